@@ -1,0 +1,240 @@
+/*
+ * lmcache_amd.h — C ABI of the MI355X (gfx950) KV-transfer, CacheGen and
+ * fused K-RoPE library (liblmcache_amd.so).
+ *
+ * Every entry point takes plain pointers, sizes and a hipStream_t passed as
+ * `void *`; there are no torch types in any signature.  Tensors cross the
+ * boundary as `lmc_tensor` descriptors (data pointer, dtype, device, sizes,
+ * strides — the same facts the reference host code reads from a
+ * torch::Tensor).  Work is enqueued asynchronously on `stream`; callers keep
+ * every buffer alive until the stream has drained, exactly as the reference's
+ * ops require (csrc/mem_kernels.cpp:96-108 captures raw pointers in the
+ * launch lambda).
+ *
+ * Return value of every function: one of the LMC_* status codes below.  On a
+ * non-zero status `lmc_last_error()` returns a thread-local message.  The
+ * Python layer raises ValueError / RuntimeError / NotImplementedError for
+ * LMC_ERR_VALUE / LMC_ERR_RUNTIME (and LMC_ERR_HIP) / LMC_ERR_NOT_IMPLEMENTED,
+ * the exception types the reference raises (csrc/utils.cpp:903-966,
+ * TORCH_CHECK sites, csrc/mem_kernels.cpp:255-263).
+ */
+#ifndef LMCACHE_AMD_H
+#define LMCACHE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lmc_status {
+  LMC_OK = 0,
+  LMC_ERR_VALUE = 1,           /* bad argument value (Python ValueError)        */
+  LMC_ERR_RUNTIME = 2,         /* failed check (Python RuntimeError)            */
+  LMC_ERR_NOT_IMPLEMENTED = 3, /* Python NotImplementedError                    */
+  LMC_ERR_HIP = 4              /* HIP runtime error (Python RuntimeError)       */
+};
+
+enum lmc_dtype {
+  LMC_U8 = 0,
+  LMC_I8 = 1,
+  LMC_I16 = 2,
+  LMC_I32 = 3,
+  LMC_I64 = 4,
+  LMC_F16 = 5,
+  LMC_BF16 = 6,
+  LMC_F32 = 7
+};
+
+/* KV cache storage formats; the integer values are the reference's
+ * KVCacheFormat contract (lmcache_ascend/v1/kv_format.py:13-83). */
+enum lmc_kv_format {
+  LMC_FMT_UNDEFINED = 0,
+  LMC_FMT_MERGED_KV = 1,
+  LMC_FMT_SEPARATE_KV = 2,
+  LMC_FMT_MLA_KV = 3,
+  LMC_FMT_DSA_KV = 4,
+  LMC_FMT_MLA_LATENT = 5,
+  LMC_FMT_DSA_INDEX = 6
+};
+
+#define LMC_MAX_DIMS 6
+
+/* A strided tensor.  `data` is the address of element 0: a device address
+ * when device >= 0, a host address when device == -1 (pinned host memory is
+ * translated to its device mapping by the library, like the reference's
+ * get_kernel_ptr, csrc/utils.h:32-51).  Strides are in elements. */
+typedef struct lmc_tensor {
+  void *data;
+  int32_t dtype;
+  int32_t device;
+  int32_t ndim;
+  int32_t reserved;
+  int64_t sizes[LMC_MAX_DIMS];
+  int64_t strides[LMC_MAX_DIMS];
+} lmc_tensor;
+
+/* Thread-local text of the last error raised on this thread. */
+const char *lmc_last_error(void);
+
+/* Library version string. */
+const char *lmc_version(void);
+
+/* ------------------------------------------------------------------------
+ * Paged-KV gather / scatter
+ * ------------------------------------------------------------------------ */
+
+/* Replaces multi_layer_kv_transfer (csrc/mem_kernels.cpp:75-111; planner
+ * csrc/utils.cpp:29-154; pybind csrc/pybind.cpp:364).
+ * key_value: LMCache memory object, [kv, L, T, W] (device or pinned host).
+ * key_value_ptrs: device int64 table of paged-cache base addresses.
+ * direction != 0: paged -> key_value (store); 0: key_value -> paged. */
+int lmc_multi_layer_kv_transfer(const lmc_tensor *key_value,
+                                const lmc_tensor *key_value_ptrs,
+                                const lmc_tensor *slot_mapping,
+                                int32_t paged_device, int64_t page_buffer_size,
+                                int32_t direction, int32_t use_mla,
+                                int32_t kvcache_format, int64_t k_hidden_dims,
+                                int64_t v_hidden_dims, int64_t dsa_hidden_dims,
+                                void *stream);
+
+/* Batched form of lmc_multi_layer_kv_transfer: `n_chunks` memory objects
+ * (`chunks[i]`, each [kv, L, T_i, W]) that cover the token ranges
+ * [token_starts[i], token_starts[i] + T_i) of `slot_mapping`, moved by one
+ * kernel launch per 64 chunks.  It replaces the per-chunk launch loop of the
+ * reference's caller (lmcache_ascend/v1/npu_connector/npu_connectors.py:
+ * 1278-1284 and 1465-1469); each chunk's bytes are identical to a
+ * lmc_multi_layer_kv_transfer call on that chunk.  token_starts is a host
+ * array. */
+int lmc_multi_layer_kv_transfer_batched(
+    const lmc_tensor *chunks, int32_t n_chunks, const int64_t *token_starts,
+    const lmc_tensor *key_value_ptrs, const lmc_tensor *slot_mapping,
+    int32_t paged_device, int64_t page_buffer_size, int32_t direction,
+    int32_t use_mla, int32_t kvcache_format, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
+
+/* Replaces fused_multi_layer_kv_transfer (csrc/mem_kernels.cpp:113-213;
+ * pybind csrc/pybind.cpp:365): the gather/scatter runs against the device
+ * `staging_cache`, and one DMA copy moves required_size bytes between the
+ * staging buffer and the host buffer `key_value` (after the kernel for
+ * direction != 0, before it for direction == 0). */
+int lmc_fused_multi_layer_kv_transfer(
+    const lmc_tensor *key_value, const lmc_tensor *staging_cache,
+    const lmc_tensor *key_value_ptrs, const lmc_tensor *slot_mapping,
+    int32_t paged_device, int64_t page_buffer_size, int32_t direction,
+    int32_t use_mla, int32_t kvcache_format, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
+
+/* Replaces single_layer_kv_transfer (csrc/mem_kernels.cpp:265-334; planner
+ * csrc/utils.cpp:212-406; validation csrc/utils.cpp:903-966; pybind
+ * csrc/pybind.cpp:467-472).  `caches` holds the n_caches paged tensors of
+ * one layer (MERGED: 1; SEPARATE: K, V; MLA: K, V; DSA_KV: K, V, DSA;
+ * DSA_INDEX: indexer). */
+int lmc_single_layer_kv_transfer(const lmc_tensor *lmc_key_value_cache,
+                                 const lmc_tensor *caches, int32_t n_caches,
+                                 const lmc_tensor *slot_mapping,
+                                 int32_t direction, int32_t kvcache_format,
+                                 int32_t token_major, int32_t vllm_two_major,
+                                 int64_t k_hidden_dims, int64_t v_hidden_dims,
+                                 int64_t dsa_hidden_dims, void *stream);
+
+/* Replaces load_and_reshape_flash (csrc/mem_kernels.cpp:1341-1387; pybind
+ * csrc/pybind.cpp:475): layer `layer_idx` of key_value [2, L, T, W] is
+ * filled from key_cache / value_cache rows slot_mapping[t]. */
+int lmc_load_and_reshape_flash(const lmc_tensor *key_value,
+                               const lmc_tensor *key_cache,
+                               const lmc_tensor *value_cache,
+                               const lmc_tensor *slot_mapping,
+                               int32_t layer_idx, void *stream);
+
+/* Replaces reshape_and_cache_back_flash (csrc/mem_kernels.cpp:1389-1440;
+ * pybind csrc/pybind.cpp:476): the inverse of lmc_load_and_reshape_flash. */
+int lmc_reshape_and_cache_back_flash(const lmc_tensor *key_value,
+                                     const lmc_tensor *key_cache,
+                                     const lmc_tensor *value_cache,
+                                     const lmc_tensor *slot_mapping,
+                                     int32_t layer_idx, void *stream);
+
+/* ------------------------------------------------------------------------
+ * CacheGen codec
+ * ------------------------------------------------------------------------ */
+
+/* Replaces calculate_cdf (csrc/cachegen_kernels.cpp:119-155; pybind
+ * csrc/pybind.cpp:480).  input: [L, T, C] u8/i8 symbols.  output: a
+ * caller-allocated int16 [L, C, n_bins + 1] tensor (the reference allocates
+ * it with torch::zeros; the Python layer does the same before this call). */
+int lmc_calculate_cdf(const lmc_tensor *input, int32_t n_bins,
+                      const lmc_tensor *output, void *stream);
+
+/* Replaces encode_fast_new (csrc/cachegen_kernels.cpp:17-58; pybind
+ * csrc/pybind.cpp:477). */
+int lmc_encode_fast_new(const lmc_tensor *cdf, const lmc_tensor *input_sym,
+                        const lmc_tensor *output_buffer,
+                        const lmc_tensor *output_lengths, void *stream);
+
+/* Replaces decode_fast_new (csrc/cachegen_kernels.cpp:60-65; pybind
+ * csrc/pybind.cpp:478); like the reference it always returns
+ * LMC_ERR_NOT_IMPLEMENTED. */
+int lmc_decode_fast_new(const lmc_tensor *cdf, const lmc_tensor *bytestreams,
+                        const lmc_tensor *lengths, const lmc_tensor *output,
+                        void *stream);
+
+/* Replaces decode_fast_prefsum (csrc/cachegen_kernels.cpp:67-112; pybind
+ * csrc/pybind.cpp:479). */
+int lmc_decode_fast_prefsum(const lmc_tensor *cdf,
+                            const lmc_tensor *bytestreams,
+                            const lmc_tensor *lengths,
+                            const lmc_tensor *output, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Fused K re-rotation (CacheBlend)
+ * ------------------------------------------------------------------------ */
+
+/* Replaces rotary_embedding_k_fused (csrc/pos_kernels.cpp:158-196; pybind
+ * csrc/pybind.cpp:481): key [T, H*head_size] is rotated in place from
+ * old_positions to new_positions with the [max_pos, rot] cos|sin cache. */
+int lmc_rotary_embedding_k_fused(const lmc_tensor *old_positions,
+                                 const lmc_tensor *new_positions,
+                                 const lmc_tensor *key, int64_t head_size,
+                                 const lmc_tensor *cos_sin_cache,
+                                 int32_t is_neox, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Pinned host memory and device address translation
+ * ------------------------------------------------------------------------ */
+
+/* Replaces get_device_ptr (csrc/common/managed_mem.cpp:189-236; pybind
+ * csrc/pybind.cpp:330-336): device address of host address `host_ptr`
+ * valid for `required_size` bytes, or 0 when the range is not mapped. */
+int lmc_get_device_ptr(uintptr_t host_ptr, size_t required_size,
+                       uintptr_t *out_device_ptr);
+
+/* Replaces register_mapping (csrc/common/managed_mem.cpp:395-407; pybind
+ * csrc/pybind.cpp:337-342): records host->device for `size` bytes. */
+int lmc_register_mapping(uintptr_t host_ptr, uintptr_t dev_ptr, size_t size,
+                         uintptr_t *out_device_ptr);
+
+/* Replaces unregister_ptr (csrc/common/managed_mem.cpp:409-422; pybind
+ * csrc/pybind.cpp:343-345).  *out_status is
+ * 0 when a mapping was removed, -1 when none existed. */
+int lmc_unregister_ptr(uintptr_t host_ptr, int32_t *out_status);
+
+/* Replaces alloc_pinned_ptr (csrc/common/mem_alloc.cpp:19-44; pybind
+ * csrc/pybind.cpp:346-347): page-locked host memory mapped into the device
+ * address space and recorded for lmc_get_device_ptr. */
+int lmc_alloc_pinned_ptr(size_t size, uint32_t flags, uintptr_t *out_ptr);
+
+/* Replaces free_pinned_ptr (csrc/common/mem_alloc.cpp:46-52; pybind
+ * csrc/pybind.cpp:348). */
+int lmc_free_pinned_ptr(uintptr_t ptr);
+
+/* Replaces get_gpu_pci_bus_id (pybind csrc/pybind.cpp:482): the PCI bus id
+ * string of `device`, written NUL-terminated into buf[0..buf_len). */
+int lmc_get_gpu_pci_bus_id(int32_t device, char *buf, int32_t buf_len);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* LMCACHE_AMD_H */

@@ -1,0 +1,843 @@
+// Paged-KV gather / scatter for MI355X (gfx950).
+//
+// One kernel family serves every gather/scatter entry point of the
+// reference's c_ops surface: multi_layer_kv_transfer (and its batched and
+// staged "fused" forms), single_layer_kv_transfer, load_and_reshape_flash and
+// reshape_and_cache_back_flash.  Each of them is a pure byte copy of rows:
+// for every (plane p, layer l, token t) with s = slot_mapping[t],
+//
+//     LMC row (p, l, t)  <->  paged row (l, p, s)
+//
+// (reference docstring csrc/mem_kernels.cpp:54-74).  The host planner below
+// turns a call's tensors into a CopyJob: per plane, the byte geometry of the
+// LMCache side (plane / layer / token strides) and of the paged side (base
+// pointer, block stride, row pitch).  The planner follows the reference's
+// layout derivation (csrc/utils.cpp:29-86 for the multi-layer formats,
+// csrc/utils.cpp:212-406 for the single-layer strides); the device side is
+// written for CDNA4 rather than following the AscendC UB tiling:
+//
+//  * one wavefront owns a whole row, so the row index, the slot lookup and
+//    all address arithmetic are wave-uniform scalar work;
+//  * the 64 lanes move the row with 16-byte accesses (1 KiB per wave
+//    instruction); each wave keeps ROWS_PER_WAVE rows x SEGS accesses in
+//    flight per lane before the first store;
+//  * grid.y enumerates LMCache chunks (memory objects), so a whole batch of
+//    chunks is one launch; grid.x strides over rows.
+//
+// Slots outside [0, num_slots) are skipped: no read and no write.  The
+// reference states that -1 never reaches its kernels
+// (lmcache_ascend/v1/npu_connector/npu_connectors.py:1106-1112) while its
+// in-tree kernels and CPU substitutes skip negative slots
+// (csrc/graph/sparse_graph_kernel.cpp:45-48, tools/cpu_vllm_runtime.py:
+// 379-380); skipping is the superset.
+#include "common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+namespace lmc {
+
+constexpr int kMaxPlanes = 3;
+constexpr int kMaxChunks = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRowsPerWave = 2;
+constexpr int kSegs = 2;
+
+// Byte geometry of one plane (K, V or DSA) of a copy.
+struct PlaneDesc {
+  int64_t row_bytes;           // bytes per row
+  // LMCache side.  Offsets depend on the chunk's token count T (multi-layer
+  // memory objects are [kv, L, T, W]), so each is fixed + per_T * T.
+  int64_t lmc_off_fixed;
+  int64_t lmc_off_per_t;
+  int64_t lmc_layer_fixed;
+  int64_t lmc_layer_per_t;
+  int64_t lmc_token_stride;
+  // Paged side: row(s) = base + paged_off + (s / BS) * blk_stride
+  //                                        + (s % BS) * row_pitch
+  // or, with block_size == 0, base + paged_off + s * row_pitch.
+  int64_t paged_off;
+  int64_t blk_stride;
+  int64_t row_pitch;
+};
+
+struct CopyJob {
+  PlaneDesc plane[kMaxPlanes];
+  uint64_t base[kMaxPlanes];   // paged base per plane when table == nullptr
+  const uint64_t *table;       // per-layer pointer table (multi-layer ops)
+  int32_t table_ppl;           // pointers per layer in `table`
+  int32_t table_idx[kMaxPlanes];
+  const void *slots;           // slot_mapping (already offset to token 0)
+  int32_t slot_i32;
+  int32_t n_planes;
+  int32_t n_layers;
+  int32_t block_size;          // 0: flat rows
+  int64_t num_slots;           // valid slots are [0, num_slots)
+  int32_t page2lmc;            // 1: paged -> LMC (store), 0: LMC -> paged
+  int32_t pad_;
+};
+
+struct ChunkList {
+  uint64_t lmc[kMaxChunks];       // kernel-visible LMC chunk address
+  int32_t tok_start[kMaxChunks];  // chunk c: slot_mapping[start, start+count)
+  int32_t tok_count[kMaxChunks];
+};
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int VEC> struct VecOf;
+template <> struct VecOf<16> { using T = u32x4; };
+template <> struct VecOf<8> { using T = u32x2; };
+template <> struct VecOf<4> { using T = uint32_t; };
+template <> struct VecOf<2> { using T = uint16_t; };
+template <> struct VecOf<1> { using T = uint8_t; };
+
+template <typename T, bool NT> __device__ __forceinline__ T ld(const T *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Resolves row `row` of chunk `c` to (src, dst); returns the row's byte count,
+// or 0 when the slot is skipped.  All inputs are wave-uniform.
+__device__ __forceinline__ int64_t row_ptrs(const CopyJob &job, uint8_t *lmc,
+                                            int tok0, int T, int per_plane,
+                                            int row, const uint8_t *&src,
+                                            uint8_t *&dst) {
+  const int p = row / per_plane;
+  const int rem = row - p * per_plane;
+  const int l = rem / T;
+  const int t = rem - l * T;
+  int64_t slot = job.slot_i32
+                     ? static_cast<int64_t>(
+                           static_cast<const int32_t *>(job.slots)[tok0 + t])
+                     : static_cast<const int64_t *>(job.slots)[tok0 + t];
+  slot = __builtin_amdgcn_readfirstlane(static_cast<int>(slot)) |
+         (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
+              static_cast<int>(slot >> 32)))
+          << 32);
+  if (slot < 0 || slot >= job.num_slots) return 0;
+  const PlaneDesc &pd = job.plane[p];
+  uint64_t pbase;
+  if (job.table != nullptr) {
+    pbase = job.table[static_cast<int64_t>(l) * job.table_ppl +
+                      job.table_idx[p]];
+    pbase = static_cast<uint32_t>(
+                __builtin_amdgcn_readfirstlane(static_cast<int>(pbase))) |
+            (static_cast<uint64_t>(static_cast<uint32_t>(
+                 __builtin_amdgcn_readfirstlane(static_cast<int>(pbase >> 32))))
+             << 32);
+  } else {
+    pbase = job.base[p];
+  }
+  int64_t poff = pd.paged_off;
+  if (job.block_size > 0) {
+    const uint32_t s32 = static_cast<uint32_t>(slot);
+    const uint32_t bs = static_cast<uint32_t>(job.block_size);
+    const uint32_t blk = s32 / bs;
+    poff += static_cast<int64_t>(blk) * pd.blk_stride +
+            static_cast<int64_t>(s32 - blk * bs) * pd.row_pitch;
+  } else {
+    poff += slot * pd.row_pitch;
+  }
+  uint8_t *paged = reinterpret_cast<uint8_t *>(pbase) + poff;
+  uint8_t *lm = lmc + pd.lmc_off_fixed + pd.lmc_off_per_t * T +
+                static_cast<int64_t>(l) *
+                    (pd.lmc_layer_fixed + pd.lmc_layer_per_t * T) +
+                static_cast<int64_t>(t) * pd.lmc_token_stride;
+  if (job.page2lmc) {
+    src = paged;
+    dst = lm;
+  } else {
+    src = lm;
+    dst = paged;
+  }
+  return pd.row_bytes;
+}
+
+template <int VEC, bool NT>
+__global__ void __launch_bounds__(kThreads)
+    kv_rows_copy(const CopyJob job, const ChunkList chunks) {
+  using V = typename VecOf<VEC>::T;
+  const int c = blockIdx.y;
+  const int tok0 = chunks.tok_start[c];
+  const int T = chunks.tok_count[c];
+  const int per_plane = job.n_layers * T;
+  const int rows = job.n_planes * per_plane;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t *lmc = reinterpret_cast<uint8_t *>(chunks.lmc[c]);
+  const int step = gridDim.x * kWaves * kRowsPerWave;
+
+  for (int r0 = (blockIdx.x * kWaves + wave) * kRowsPerWave; r0 < rows;
+       r0 += step) {
+    const uint8_t *src[kRowsPerWave];
+    uint8_t *dst[kRowsPerWave];
+    int64_t nb[kRowsPerWave];
+    int64_t nb_max = 0;
+    bool slow = false;
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+      nb[r] = 0;
+      src[r] = nullptr;
+      dst[r] = nullptr;
+      if (r0 + r < rows)
+        nb[r] = row_ptrs(job, lmc, tok0, T, per_plane, r0 + r, src[r], dst[r]);
+      // The host checked every alignment it can see; a table entry (a device
+      // value) that is not VEC-aligned sends the row to the byte path.
+      if (nb[r] > 0 &&
+          ((reinterpret_cast<uintptr_t>(src[r]) |
+            reinterpret_cast<uintptr_t>(dst[r])) &
+           (VEC - 1)) != 0) {
+        slow = true;
+      }
+      nb_max = nb[r] > nb_max ? nb[r] : nb_max;
+    }
+    if (slow) {
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r)
+        for (int64_t o = lane; o < nb[r]; o += 64) dst[r][o] = src[r][o];
+      continue;
+    }
+    for (int64_t base = 0; base < nb_max; base += 64 * VEC * kSegs) {
+      V v[kRowsPerWave][kSegs];
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+        for (int s = 0; s < kSegs; ++s) {
+          const int64_t o = base + (s * 64 + lane) * VEC;
+          if (o < nb[r])
+            v[r][s] = ld<V, NT>(reinterpret_cast<const V *>(src[r] + o));
+        }
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+        for (int s = 0; s < kSegs; ++s) {
+          const int64_t o = base + (s * 64 + lane) * VEC;
+          if (o < nb[r]) st<V, NT>(reinterpret_cast<V *>(dst[r] + o), v[r][s]);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+namespace {
+
+int64_t gcd64(int64_t a, int64_t b) {
+  a = a < 0 ? -a : a;
+  b = b < 0 ? -b : b;
+  while (b) {
+    int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// Largest access width (16/8/4/2/1 bytes) dividing every host-visible offset,
+// stride and address of the job.
+int pick_vec(const CopyJob &job, const ChunkList &chunks, int n_chunks) {
+  int64_t g = 16;
+  auto fold = [&](int64_t v) { g = gcd64(g, v); };
+  for (int p = 0; p < job.n_planes; ++p) {
+    const PlaneDesc &d = job.plane[p];
+    fold(d.row_bytes);
+    fold(d.lmc_off_fixed);
+    fold(d.lmc_off_per_t);
+    fold(d.lmc_layer_fixed);
+    fold(d.lmc_layer_per_t);
+    fold(d.lmc_token_stride);
+    fold(d.paged_off);
+    fold(d.blk_stride);
+    fold(d.row_pitch);
+    if (job.table == nullptr) fold(static_cast<int64_t>(job.base[p] & 0xff));
+  }
+  for (int c = 0; c < n_chunks; ++c)
+    fold(static_cast<int64_t>(chunks.lmc[c] & 0xff));
+  if (g == 0) g = 16;
+  if (g % 16 == 0) return 16;
+  if (g % 8 == 0) return 8;
+  if (g % 4 == 0) return 4;
+  if (g % 2 == 0) return 2;
+  return 1;
+}
+
+template <int VEC>
+void launch_vec(const CopyJob &job, const ChunkList &chunks, int n_chunks,
+                int max_rows, bool nt, hipStream_t stream) {
+  const int rows_per_block = kWaves * kRowsPerWave;
+  int gx = (max_rows + rows_per_block - 1) / rows_per_block;
+  gx = std::max(1, std::min(gx, 65535));
+  dim3 grid(gx, n_chunks), block(kThreads);
+  if (nt)
+    hipLaunchKernelGGL((kv_rows_copy<VEC, true>), grid, block, 0, stream, job,
+                       chunks);
+  else
+    hipLaunchKernelGGL((kv_rows_copy<VEC, false>), grid, block, 0, stream, job,
+                       chunks);
+}
+
+bool nontemporal_enabled() {
+  static const bool on = [] {
+    const char *e = std::getenv("LMC_AMD_NONTEMPORAL");
+    return e == nullptr || e[0] != '0';
+  }();
+  return on;
+}
+
+// Launches one copy over `n` chunks (split into launches of kMaxChunks).
+// `host_lmc`: the LMCache side is page-locked host memory reached over PCIe;
+// the streaming (non-temporal) cache hints are used for HBM-only copies.
+void launch_copy(const CopyJob &job, const std::vector<uint64_t> &lmc_ptrs,
+                 const std::vector<int64_t> &tok_starts,
+                 const std::vector<int64_t> &tok_counts, bool host_lmc,
+                 hipStream_t stream) {
+  const size_t n = lmc_ptrs.size();
+  const int64_t slot_es = job.slot_i32 ? 4 : 8;
+  for (size_t c0 = 0; c0 < n; c0 += kMaxChunks) {
+    const int nc = static_cast<int>(std::min<size_t>(kMaxChunks, n - c0));
+    // Rebase the slot pointer to the smallest start of this group so the
+    // per-chunk token offsets fit 32-bit kernel arithmetic.
+    int64_t base_tok = tok_starts[c0];
+    for (int i = 1; i < nc; ++i) base_tok = std::min(base_tok, tok_starts[c0 + i]);
+    CopyJob j = job;
+    j.slots = static_cast<const uint8_t *>(job.slots) + base_tok * slot_es;
+    ChunkList cl;
+    std::memset(&cl, 0, sizeof(cl));
+    int max_rows = 0;
+    for (int i = 0; i < nc; ++i) {
+      const int64_t rel = tok_starts[c0 + i] - base_tok;
+      const int64_t cnt = tok_counts[c0 + i];
+      const int64_t rows = cnt * job.n_layers * job.n_planes;
+      check(rel + cnt < (int64_t(1) << 31) && rows < (int64_t(1) << 31),
+            "chunk does not fit 32-bit row indexing");
+      cl.lmc[i] = lmc_ptrs[c0 + i];
+      cl.tok_start[i] = static_cast<int32_t>(rel);
+      cl.tok_count[i] = static_cast<int32_t>(cnt);
+      max_rows = std::max<int>(max_rows, static_cast<int>(rows));
+    }
+    if (max_rows == 0) continue;
+    const int vec = pick_vec(j, cl, nc);
+    const bool nt = nontemporal_enabled() && !host_lmc;
+    switch (vec) {
+    case 16: launch_vec<16>(j, cl, nc, max_rows, nt, stream); break;
+    case 8: launch_vec<8>(j, cl, nc, max_rows, nt, stream); break;
+    case 4: launch_vec<4>(j, cl, nc, max_rows, nt, stream); break;
+    case 2: launch_vec<2>(j, cl, nc, max_rows, nt, stream); break;
+    default: launch_vec<1>(j, cl, nc, max_rows, nt, stream); break;
+    }
+    hip_check(hipGetLastError(), "kv_rows_copy launch");
+  }
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+const lmc_tensor &slots_of(const lmc_tensor *s) {
+  const lmc_tensor &t = deref(s, "slot_mapping");
+  check(t.ndim == 1, "slot_mapping must be 1-D");
+  check(t.dtype == LMC_I64 || t.dtype == LMC_I32,
+        "slot_mapping must be int64 or int32");
+  check(t.sizes[0] <= 1 || t.strides[0] == 1,
+        "slot_mapping must be contiguous");
+  return t;
+}
+
+// --- multi-layer planning (csrc/utils.cpp:29-86) ---------------------------
+
+struct MultiLayerGeom {
+  CopyJob job;                 // LMC geometry is per-T (filled per chunk)
+  int64_t lmc_bytes_per_token; // LMC bytes one token occupies (all planes,
+                               // all layers)
+  int n_planes;
+};
+
+MultiLayerGeom plan_multi_layer(int64_t n_layers, int64_t last_dim,
+                                int64_t es, const lmc_tensor &ptrs,
+                                int64_t page_buffer_size, bool direction,
+                                bool use_mla, int fmt, int64_t kH, int64_t vH,
+                                int64_t dsaH) {
+  MultiLayerGeom g;
+  std::memset(&g, 0, sizeof(g));
+  CopyJob &job = g.job;
+  int64_t width[kMaxPlanes] = {0, 0, 0};
+  int64_t paged_off[kMaxPlanes] = {0, 0, 0};
+  int idx[kMaxPlanes] = {0, 0, 0};
+  int planes = 0, ppl = 0;
+  bool concatenated = false;  // [1, L, T, sum(W)] rows vs [P, L, T, W]
+  switch (fmt) {
+  case LMC_FMT_MERGED_KV:
+    if (use_mla) {
+      // Single-plane MLA latent cache: one [NB, BS, W] tensor per layer
+      // (the upstream-LMCache use_mla meaning, also the MindSpore host path,
+      // csrc/mindspore/mem_kernels.cpp:85-88).
+      planes = 1; ppl = 1; width[0] = last_dim;
+    } else {
+      // ptrs[l] -> [2, NB, BS, H, D]; V plane follows page_buffer_size rows
+      // of K (csrc/mem_kernels.cpp:58-69).
+      planes = 2; ppl = 1; width[0] = width[1] = last_dim;
+      idx[1] = 0;
+      paged_off[1] = page_buffer_size * last_dim * es;
+    }
+    break;
+  case LMC_FMT_SEPARATE_KV:
+    if (use_mla) {
+      planes = 1; ppl = 1; width[0] = last_dim;
+    } else {
+      planes = 2; ppl = 2; width[0] = width[1] = last_dim;
+      idx[1] = 1;
+    }
+    break;
+  case LMC_FMT_MLA_KV:
+  case LMC_FMT_MLA_LATENT:
+    planes = 2; ppl = 2; width[0] = kH; width[1] = vH; idx[1] = 1;
+    concatenated = true;
+    break;
+  case LMC_FMT_DSA_KV:
+    planes = 3; ppl = 3; width[0] = kH; width[1] = vH; width[2] = dsaH;
+    idx[1] = 1; idx[2] = 2;
+    concatenated = true;
+    break;
+  case LMC_FMT_DSA_INDEX:
+    planes = 1; ppl = 1; width[0] = dsaH;
+    concatenated = true;
+    break;
+  default:
+    fail(LMC_ERR_RUNTIME, "Unsupported KVCacheFormat: " + std::to_string(fmt));
+  }
+  for (int p = 0; p < planes; ++p)
+    check(width[p] > 0, "hidden dims must be positive for KV format " +
+                            std::to_string(fmt));
+  check(page_buffer_size > 0, "page_buffer_size must be positive");
+  check(ptrs.dtype == LMC_I64 && ptrs.ndim == 1,
+        "key_value_ptrs must be a 1-D int64 tensor");
+  check(ptrs.device >= 0, "key_value_ptrs must be a device tensor");
+  check(ptrs.sizes[0] >= n_layers * ppl,
+        "key_value_ptrs has " + std::to_string(ptrs.sizes[0]) +
+            " entries, need " + std::to_string(n_layers * ppl));
+  check(ptrs.sizes[0] <= 1 || ptrs.strides[0] == 1,
+        "key_value_ptrs must be contiguous");
+
+  int64_t wsum = 0;
+  for (int p = 0; p < planes; ++p) wsum += width[p];
+  int64_t col = 0;
+  for (int p = 0; p < planes; ++p) {
+    PlaneDesc &d = job.plane[p];
+    d.row_bytes = width[p] * es;
+    if (concatenated) {
+      d.lmc_off_fixed = col * es;
+      d.lmc_layer_per_t = wsum * es;
+      d.lmc_token_stride = wsum * es;
+    } else {
+      d.lmc_off_per_t = static_cast<int64_t>(p) * n_layers * width[p] * es;
+      d.lmc_layer_per_t = width[p] * es;
+      d.lmc_token_stride = width[p] * es;
+    }
+    d.paged_off = paged_off[p];
+    d.row_pitch = width[p] * es;
+    d.blk_stride = 0;
+    job.table_idx[p] = idx[p];
+    col += width[p];
+  }
+  job.table = reinterpret_cast<const uint64_t *>(ptrs.data);
+  job.table_ppl = ppl;
+  job.n_planes = planes;
+  job.n_layers = static_cast<int32_t>(n_layers);
+  job.block_size = 0;
+  job.num_slots = page_buffer_size;
+  job.page2lmc = direction ? 1 : 0;
+  g.n_planes = planes;
+  g.lmc_bytes_per_token = n_layers * wsum * es;
+  return g;
+}
+
+void run_multi_layer(const lmc_tensor *chunks, int n_chunks,
+                     const int64_t *token_starts, const lmc_tensor *ptrs_t,
+                     const lmc_tensor *slots_t, int paged_device,
+                     int64_t page_buffer_size, bool direction, bool use_mla,
+                     int fmt, int64_t kH, int64_t vH, int64_t dsaH,
+                     hipStream_t stream, bool batched) {
+  check(n_chunks >= 0, "n_chunks must be non-negative");
+  if (n_chunks == 0) return;
+  const lmc_tensor &ptrs = deref(ptrs_t, "key_value_ptrs");
+  const lmc_tensor &slots = slots_of(slots_t);
+  const lmc_tensor &first = deref(&chunks[0], "key_value");
+  check(first.ndim >= 2, "key_value must have at least 2 dims");
+  const int64_t n_layers = size(first, 1);
+  const int64_t last_dim = size(first, -1);
+  const int64_t es = elem_size(first);
+  MultiLayerGeom g = plan_multi_layer(n_layers, last_dim, es, ptrs,
+                                      page_buffer_size, direction, use_mla,
+                                      fmt, kH, vH, dsaH);
+  DeviceGuard guard(paged_device >= 0 ? paged_device : ptrs.device);
+  g.job.slots = kernel_ptr(slots);
+  g.job.slot_i32 = slots.dtype == LMC_I32;
+
+  std::vector<uint64_t> lmc_ptrs(n_chunks);
+  std::vector<int64_t> starts(n_chunks), counts(n_chunks);
+  bool host_lmc = false;
+  for (int c = 0; c < n_chunks; ++c) {
+    const lmc_tensor &kv = deref(&chunks[c], "key_value");
+    check(kv.ndim >= 2 && size(kv, 1) == n_layers && size(kv, -1) == last_dim &&
+              elem_size(kv) == es,
+          "all memory objects of a batch must share layers, width and dtype");
+    // The reference takes the token count from slot_mapping for a single
+    // call (csrc/utils.cpp:43) and ignores key_value's strides, treating the
+    // object as a flat [kv, L, T, W] buffer (csrc/mem_kernels.cpp:83).
+    const int64_t T = batched ? size(kv, -2) : slots.sizes[0];
+    const int64_t start = batched ? token_starts[c] : 0;
+    check(start >= 0 && start + T <= slots.sizes[0],
+          "chunk token range exceeds slot_mapping");
+    const int64_t need = T * g.lmc_bytes_per_token;
+    check(nbytes(kv) >= need,
+          "key_value holds " + std::to_string(nbytes(kv)) +
+              " bytes, the transfer needs " + std::to_string(need));
+    lmc_ptrs[c] = reinterpret_cast<uint64_t>(
+        T > 0 ? kernel_ptr(kv) : static_cast<uint8_t *>(kv.data));
+    starts[c] = start;
+    counts[c] = T;
+    host_lmc = host_lmc || kv.device < 0;
+  }
+  launch_copy(g.job, lmc_ptrs, starts, counts, host_lmc, stream);
+}
+
+// --- single-layer planning (csrc/utils.cpp:212-406, 903-966) ---------------
+
+void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt) {
+  if (fmt != LMC_FMT_MERGED_KV && fmt != LMC_FMT_SEPARATE_KV &&
+      fmt != LMC_FMT_MLA_KV && fmt != LMC_FMT_DSA_KV &&
+      fmt != LMC_FMT_MLA_LATENT && fmt != LMC_FMT_DSA_INDEX)
+    fail(LMC_ERR_VALUE,
+         "Invalid KV cache format: " + std::to_string(fmt) +
+             ". Expected 1 (MERGED_KV), 2 (SEPARATE_KV), 3 (MLA_KV), 4 "
+             "(DSA_KV), 5 (MLA_LATENT), or 6 (DSA_INDEX)");
+  if (n <= 0) fail(LMC_ERR_VALUE, "vllm_kv_caches cannot be empty");
+  auto same_sizes = [](const lmc_tensor &a, const lmc_tensor &b) {
+    if (a.ndim != b.ndim) return false;
+    for (int i = 0; i < a.ndim; ++i)
+      if (a.sizes[i] != b.sizes[i]) return false;
+    return true;
+  };
+  if (fmt == LMC_FMT_DSA_KV) {
+    if (n != 3) fail(LMC_ERR_VALUE, "DSA_KV expects 3 tensors (K, V, and DSA_K).");
+  } else if (fmt == LMC_FMT_MLA_KV || fmt == LMC_FMT_MLA_LATENT) {
+    if (n < 2)
+      fail(LMC_ERR_VALUE, "MLA_KV/MLA_LATENT expects 2 tensors (K and V).");
+    if (same_sizes(caches[0], caches[1]))
+      fail(LMC_ERR_VALUE, "MLA_KV/MLA_LATENT expects K and V caches to have "
+                          "different shapes.");
+  } else if (fmt == LMC_FMT_DSA_INDEX) {
+    // at least one tensor: already checked
+  } else if (fmt == LMC_FMT_SEPARATE_KV) {
+    if (n != 2) fail(LMC_ERR_VALUE, "SEPARATE_KV expects 2 tensors (K and V).");
+    if (!same_sizes(caches[0], caches[1]))
+      fail(LMC_ERR_VALUE, "K and V caches must have the same shape.");
+  } else {
+    if (n != 1) fail(LMC_ERR_VALUE, "MERGED_KV expects 1 tensor.");
+  }
+}
+
+} // namespace
+
+void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
+                  const lmc_tensor *slots_t, bool direction, int fmt,
+                  bool token_major, bool two_major, int64_t kH, int64_t vH,
+                  int64_t dsaH, hipStream_t stream) {
+  validate_vllm_caches(caches, n, fmt);
+  const lmc_tensor &lmc = deref(lmc_t, "lmc_key_value_cache");
+  const lmc_tensor &slots = slots_of(slots_t);
+  const lmc_tensor &k = deref(&caches[0], "vllm_kv_caches[0]");
+  DeviceGuard guard(k.device);
+  const int64_t es = elem_size(k);
+  check(elem_size(lmc) == es, "LMC buffer and paged cache dtypes differ");
+  const int64_t T = slots.sizes[0];
+
+  CopyJob job;
+  std::memset(&job, 0, sizeof(job));
+  job.table = nullptr;
+  job.slots = kernel_ptr(slots);
+  job.slot_i32 = slots.dtype == LMC_I32;
+  job.n_layers = 1;
+  job.page2lmc = direction ? 1 : 0;
+
+  const bool mla_dsa = fmt == LMC_FMT_MLA_KV || fmt == LMC_FMT_DSA_KV ||
+                       fmt == LMC_FMT_MLA_LATENT || fmt == LMC_FMT_DSA_INDEX;
+  if (mla_dsa) {
+    // Hidden-dim defaults (csrc/utils.cpp:319-339).
+    const lmc_tensor *v = nullptr, *dsa = nullptr;
+    if (fmt != LMC_FMT_DSA_INDEX) v = &caches[1];
+    if (fmt == LMC_FMT_DSA_KV) dsa = &caches[2];
+    check(k.ndim >= 2, "paged cache must have at least 2 dims");
+    if (kH <= 0) kH = size(k, -2) * size(k, -1);
+    if (vH <= 0 && v != nullptr) vH = size(*v, -2) * size(*v, -1);
+    if (dsaH <= 0 && dsa != nullptr) dsaH = size(*dsa, -2) * size(*dsa, -1);
+    if (fmt == LMC_FMT_DSA_INDEX) {
+      kH = dsaH > 0 ? dsaH : size(k, -2) * size(k, -1);
+      vH = 0;
+    }
+    const lmc_tensor *tens[kMaxPlanes] = {&k, v, dsa};
+    int64_t w[kMaxPlanes] = {kH, fmt == LMC_FMT_DSA_INDEX ? 0 : vH,
+                             fmt == LMC_FMT_DSA_KV ? dsaH : 0};
+    int64_t plane_elems = w[0] + w[1] + w[2];
+    check(plane_elems > 0, "MLA/DSA plane size must be positive");
+    // Stacked planes [K: N*kH | V: N*vH | DSA: N*dsaH] (csrc/utils.cpp:
+    // 222-224, 241-244, 350-357).
+    const int64_t N = numel(lmc) / plane_elems;
+    check(T <= N, "LMC buffer holds " + std::to_string(N) +
+                      " tokens, slot_mapping has " + std::to_string(T));
+    int planes = 0;
+    int64_t off = 0;
+    int64_t num_slots = INT64_MAX;
+    for (int p = 0; p < kMaxPlanes; ++p) {
+      if (w[p] <= 0 || tens[p] == nullptr) { off += N * w[p]; continue; }
+      PlaneDesc &d = job.plane[planes];
+      d.row_bytes = w[p] * es;
+      d.lmc_off_fixed = off * es;
+      d.lmc_token_stride = w[p] * es;
+      d.paged_off = 0;
+      d.row_pitch = w[p] * es;
+      job.base[planes] = reinterpret_cast<uint64_t>(kernel_ptr(*tens[p]));
+      check(elem_size(*tens[p]) == es, "paged cache dtypes differ");
+      num_slots = std::min(num_slots, numel(*tens[p]) / w[p]);
+      off += N * w[p];
+      ++planes;
+    }
+    job.n_planes = planes;
+    job.block_size = 0;
+    job.num_slots = num_slots;
+  } else {
+    check(k.ndim >= 3, "paged cache must have at least 3 dims");
+    const int64_t H = size(k, -2), D = size(k, -1), BS = size(k, -3);
+    const int64_t W = H * D;
+    // LMC strides (csrc/utils.cpp:226-237): token-major [T, 2, W] or
+    // [2, T, W].
+    check(lmc.ndim >= 2, "LMC buffer must have at least 2 dims");
+    const int64_t tok_stride = token_major ? stride(lmc, 0) : stride(lmc, 1);
+    const int64_t val_off = token_major ? stride(lmc, 1) : stride(lmc, 0);
+    const int64_t lmc_need =
+        (T > 0 ? ((T - 1) * tok_stride + val_off + W) * es : 0);
+    check(lmc_need <= extent_bytes(lmc),
+          "LMC buffer is too small for " + std::to_string(T) + " tokens");
+    job.n_planes = 2;
+    job.block_size = static_cast<int32_t>(BS);
+    for (int p = 0; p < 2; ++p) {
+      PlaneDesc &d = job.plane[p];
+      d.row_bytes = W * es;
+      d.lmc_off_fixed = p == 0 ? 0 : val_off * es;
+      d.lmc_token_stride = tok_stride * es;
+      d.row_pitch = W * es;
+    }
+    if (fmt == LMC_FMT_MERGED_KV) {
+      // [2, NB, BS, H, D] (two-major) or [NB, 2, BS, H, D]
+      // (csrc/utils.cpp:249-263).
+      check(k.ndim == 5, "MERGED_KV cache must be 5-D");
+      const int64_t blk = two_major ? stride(k, 1) : stride(k, 0);
+      const int64_t voff = two_major ? stride(k, 0) : stride(k, 1);
+      const int64_t NB = two_major ? size(k, 1) : size(k, 0);
+      job.base[0] = job.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(k));
+      job.plane[0].blk_stride = job.plane[1].blk_stride = blk * es;
+      job.plane[1].paged_off = voff * es;
+      job.num_slots = NB * BS;
+    } else {
+      // SEPARATE: (K, V) each [NB, BS, H, D] (csrc/utils.cpp:266-282).
+      const lmc_tensor &v = deref(&caches[1], "vllm_kv_caches[1]");
+      check(elem_size(v) == es, "paged cache dtypes differ");
+      job.base[0] = reinterpret_cast<uint64_t>(kernel_ptr(k));
+      job.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(v));
+      job.plane[0].blk_stride = stride(k, 0) * es;
+      job.plane[1].blk_stride = stride(v, 0) * es;
+      job.num_slots = std::min(size(k, 0), size(v, 0)) * BS;
+    }
+  }
+  if (T == 0) return;
+  std::vector<uint64_t> lp{reinterpret_cast<uint64_t>(kernel_ptr(lmc))};
+  std::vector<int64_t> st{0}, ct{T};
+  launch_copy(job, lp, st, ct, lmc.device < 0, stream);
+}
+
+void flash(const lmc_tensor *kv_t, const lmc_tensor *kc_t,
+           const lmc_tensor *vc_t, const lmc_tensor *slots_t, int layer_idx,
+           bool page2lmc, hipStream_t stream) {
+  const lmc_tensor &kv = deref(kv_t, "key_value");
+  const lmc_tensor &kc = deref(kc_t, "key_cache");
+  const lmc_tensor &vc = deref(vc_t, "value_cache");
+  const lmc_tensor &slots = slots_of(slots_t);
+  DeviceGuard guard(kc.device);
+  check(kv.ndim >= 2, "key_value must be [2, L, T, W]");
+  const int64_t L = size(kv, 1), W = size(kv, -1), es = elem_size(kv);
+  const int64_t T = slots.sizes[0];
+  check(layer_idx >= 0 && layer_idx < L, "layer_idx out of range");
+  check(elem_size(kc) == es && elem_size(vc) == es, "dtype mismatch");
+  check(nbytes(kv) >= 2 * L * T * W * es, "key_value is too small");
+  CopyJob job;
+  std::memset(&job, 0, sizeof(job));
+  job.slots = kernel_ptr(slots);
+  job.slot_i32 = slots.dtype == LMC_I32;
+  job.n_layers = 1;
+  job.n_planes = 2;
+  job.block_size = 0;
+  job.page2lmc = page2lmc ? 1 : 0;
+  job.num_slots = std::min(numel(kc), numel(vc)) / W;
+  const lmc_tensor *caches[2] = {&kc, &vc};
+  for (int p = 0; p < 2; ++p) {
+    PlaneDesc &d = job.plane[p];
+    d.row_bytes = W * es;
+    d.lmc_off_fixed = (static_cast<int64_t>(p) * L + layer_idx) * T * W * es;
+    d.lmc_token_stride = W * es;
+    d.row_pitch = W * es;
+    job.base[p] = reinterpret_cast<uint64_t>(kernel_ptr(*caches[p]));
+  }
+  if (T == 0) return;
+  std::vector<uint64_t> lp{reinterpret_cast<uint64_t>(kernel_ptr(kv))};
+  std::vector<int64_t> st{0}, ct{T};
+  launch_copy(job, lp, st, ct, kv.device < 0, stream);
+}
+
+int64_t fused_required_size(int fmt, bool use_mla, int64_t L, int64_t T,
+                            int64_t W, int64_t kH, int64_t vH, int64_t dsaH,
+                            int64_t es) {
+  // csrc/mem_kernels.cpp:143-165.
+  switch (fmt) {
+  case LMC_FMT_MLA_KV:
+  case LMC_FMT_MLA_LATENT:
+    return L * T * (kH + vH) * es;
+  case LMC_FMT_DSA_KV:
+    return L * T * (kH + vH + dsaH) * es;
+  case LMC_FMT_DSA_INDEX:
+    return L * T * dsaH * es;
+  default:
+    return (use_mla ? 1 : 2) * L * T * W * es;
+  }
+}
+
+} // namespace lmc
+
+using namespace lmc;
+
+extern "C" {
+
+int lmc_multi_layer_kv_transfer(const lmc_tensor *key_value,
+                                const lmc_tensor *key_value_ptrs,
+                                const lmc_tensor *slot_mapping,
+                                int32_t paged_device, int64_t page_buffer_size,
+                                int32_t direction, int32_t use_mla,
+                                int32_t kvcache_format, int64_t k_hidden_dims,
+                                int64_t v_hidden_dims, int64_t dsa_hidden_dims,
+                                void *stream) {
+  return guarded([&] {
+    run_multi_layer(key_value, 1, nullptr, key_value_ptrs, slot_mapping,
+                    paged_device, page_buffer_size, direction != 0,
+                    use_mla != 0, kvcache_format, k_hidden_dims,
+                    v_hidden_dims, dsa_hidden_dims, as_stream(stream), false);
+  });
+}
+
+int lmc_multi_layer_kv_transfer_batched(
+    const lmc_tensor *chunks, int32_t n_chunks, const int64_t *token_starts,
+    const lmc_tensor *key_value_ptrs, const lmc_tensor *slot_mapping,
+    int32_t paged_device, int64_t page_buffer_size, int32_t direction,
+    int32_t use_mla, int32_t kvcache_format, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream) {
+  return guarded([&] {
+    check(n_chunks == 0 || (chunks != nullptr && token_starts != nullptr),
+          "chunks and token_starts are required");
+    run_multi_layer(chunks, n_chunks, token_starts, key_value_ptrs,
+                    slot_mapping, paged_device, page_buffer_size,
+                    direction != 0, use_mla != 0, kvcache_format,
+                    k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
+                    as_stream(stream), true);
+  });
+}
+
+int lmc_fused_multi_layer_kv_transfer(
+    const lmc_tensor *key_value, const lmc_tensor *staging_cache,
+    const lmc_tensor *key_value_ptrs, const lmc_tensor *slot_mapping,
+    int32_t paged_device, int64_t page_buffer_size, int32_t direction,
+    int32_t use_mla, int32_t kvcache_format, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream) {
+  return guarded([&] {
+    const lmc_tensor &kv = deref(key_value, "key_value");
+    const lmc_tensor &stg = deref(staging_cache, "staging_cache");
+    const lmc_tensor &slots = slots_of(slot_mapping);
+    check(kv.ndim >= 2, "key_value must have at least 2 dims");
+    check(stg.device >= 0, "staging_cache must be a device tensor");
+    const int64_t L = size(kv, 1), W = size(kv, -1), es = elem_size(kv);
+    const int64_t T = slots.sizes[0];
+    const int64_t required = fused_required_size(
+        kvcache_format, use_mla != 0, L, T, W, k_hidden_dims, v_hidden_dims,
+        dsa_hidden_dims, es);
+    const int64_t staging_size = nbytes(stg);
+    check(staging_size >= required,
+          "staging_cache size insufficient: need " + std::to_string(required) +
+              " bytes, got " + std::to_string(staging_size));
+    check(nbytes(kv) >= required, "key_value is smaller than the transfer");
+    hipStream_t s = as_stream(stream);
+    DeviceGuard guard(paged_device >= 0 ? paged_device : stg.device);
+    if (!direction && required > 0)
+      hip_check(hipMemcpyAsync(stg.data, kv.data, required,
+                               hipMemcpyHostToDevice, s),
+                "H2D memcpy failed: cpu_buffer -> staging_cache");
+    // The staging buffer is used as a flat buffer with key_value's logical
+    // layout from its data pointer, whatever its view strides
+    // (csrc/mem_kernels.cpp:124-126, 183-207); its capacity was checked
+    // against `required` above.
+    lmc_tensor view = kv;
+    view.data = stg.data;
+    view.device = stg.device;
+    run_multi_layer(&view, 1, nullptr, key_value_ptrs, slot_mapping,
+                    paged_device, page_buffer_size, direction != 0,
+                    use_mla != 0, kvcache_format, k_hidden_dims,
+                    v_hidden_dims, dsa_hidden_dims, s, false);
+    if (direction && required > 0)
+      hip_check(hipMemcpyAsync(kv.data, stg.data, required,
+                               hipMemcpyDeviceToHost, s),
+                "D2H memcpy failed: staging_cache -> cpu_buffer");
+  });
+}
+
+int lmc_single_layer_kv_transfer(const lmc_tensor *lmc_key_value_cache,
+                                 const lmc_tensor *caches, int32_t n_caches,
+                                 const lmc_tensor *slot_mapping,
+                                 int32_t direction, int32_t kvcache_format,
+                                 int32_t token_major, int32_t vllm_two_major,
+                                 int64_t k_hidden_dims, int64_t v_hidden_dims,
+                                 int64_t dsa_hidden_dims, void *stream) {
+  return guarded([&] {
+    single_layer(lmc_key_value_cache, caches, n_caches, slot_mapping,
+                 direction != 0, kvcache_format, token_major != 0,
+                 vllm_two_major != 0, k_hidden_dims, v_hidden_dims,
+                 dsa_hidden_dims, as_stream(stream));
+  });
+}
+
+int lmc_load_and_reshape_flash(const lmc_tensor *key_value,
+                               const lmc_tensor *key_cache,
+                               const lmc_tensor *value_cache,
+                               const lmc_tensor *slot_mapping,
+                               int32_t layer_idx, void *stream) {
+  return guarded([&] {
+    flash(key_value, key_cache, value_cache, slot_mapping, layer_idx, true,
+          as_stream(stream));
+  });
+}
+
+int lmc_reshape_and_cache_back_flash(const lmc_tensor *key_value,
+                                     const lmc_tensor *key_cache,
+                                     const lmc_tensor *value_cache,
+                                     const lmc_tensor *slot_mapping,
+                                     int32_t layer_idx, void *stream) {
+  return guarded([&] {
+    flash(key_value, key_cache, value_cache, slot_mapping, layer_idx, false,
+          as_stream(stream));
+  });
+}
+
+} // extern "C"

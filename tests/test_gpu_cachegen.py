@@ -1,0 +1,207 @@
+"""GPU parity of the CacheGen kernels (calculate_cdf, encode_fast_new,
+decode_fast_prefsum) through the C ABI.
+
+* The reference's own tests (tests/v1/test_cachegen_kernels.py) re-run on the
+  MI355X with their known answers;
+* bit-exact CDFs, bitstreams, byte lengths and decoded symbols against the
+  CPU oracle at the 32-layer x 256-token x 1024-channel K+V chunk shape
+  (K layers 0-9 quantised to 32 bins, later K layers and all V layers to 16);
+* edge cases: one token, one bin, constant channels, out-of-range symbols,
+  streams longer than the output row, and the reference's limits.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cachegen as oc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+MAX_TOKENS_PER_CHUNK = 256
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import lmcache_amd
+
+    return lmcache_amd.c_ops
+
+
+def _wrap16(values):
+    return torch.tensor(values, dtype=torch.float32).to(torch.int16)
+
+
+def _binary_stream(bits, max_sym):
+    s = "".join(format(t, f"0{bits}b") for t in range(max_sym))
+    if len(s) % 8:
+        s += "0" * (8 - len(s) % 8)
+    return [int(s[i: i + 8], 2) for i in range(0, len(s), 8)]
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+@pytest.mark.parametrize("channels", [1, 32, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6])
+def test_basic_encode(ops, layers, channels, bits):
+    """tests/v1/test_cachegen_kernels.py:31-122."""
+    max_sym = 2 ** bits
+    symbols = [s for s in range(max_sym) for _ in range(channels)] * layers
+    syms = torch.tensor(symbols).to(DEV).to(torch.int8).reshape(layers, max_sym, channels)
+    bins = max_sym + 1
+    cdf = torch.Tensor([b * (0x10000 / (bins - 1)) for b in range(bins)] * layers * channels)
+    cdf = cdf.to(DEV).to(torch.int16).reshape(layers, channels, bins)
+    out = torch.zeros(MAX_TOKENS_PER_CHUNK * layers * channels, dtype=torch.uint8).to(DEV)
+    out = out.reshape(layers, channels, MAX_TOKENS_PER_CHUNK)
+    lens = torch.zeros((layers, channels), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, syms, out, lens)
+    torch.cuda.synchronize()
+    expected = _binary_stream(bits, max_sym)
+    n = len(expected)
+    expected += [0] * (MAX_TOKENS_PER_CHUNK - n)
+    exp_t = torch.tensor(expected, dtype=torch.uint8, device=DEV).broadcast_to(out.shape)
+    assert (exp_t == out).all()
+    assert (lens == n).all()
+
+
+def test_basic_non_uniform_encode(ops):
+    """tests/v1/test_cachegen_kernels.py:125-161."""
+    syms = torch.Tensor([0, 0, 2, 3]).to(DEV).to(torch.int8).reshape(1, 4, 1)
+    cdf = torch.Tensor([0x0000, 0x8000, 0x8000, 0xC000, 0x10000]).to(DEV).to(torch.int16).reshape(1, 1, 5)
+    out = torch.zeros(4, dtype=torch.uint8, device=DEV).reshape(1, 1, 4)
+    lens = torch.zeros((1, 1), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, syms, out, lens)
+    torch.cuda.synchronize()
+    assert out[0][0][0].tolist() == int("00101100", 2)
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+@pytest.mark.parametrize("channels", [32, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
+def test_basic_decode(ops, layers, channels, bits):
+    """tests/v1/test_cachegen_kernels.py:164-239."""
+    max_sym = 2 ** bits
+    stream = _binary_stream(bits, max_sym)
+    bs = torch.tensor(stream * layers * channels, dtype=torch.uint8, device=DEV)
+    lens = torch.tensor([len(stream)] * layers * channels, dtype=torch.int32, device=DEV)
+    lens = lens.cumsum(0).to(torch.int32).reshape(layers, channels)
+    bins = max_sym + 1
+    factor = 0x10000 / (bins - 1)
+    cdf = torch.Tensor([int(b * factor) | bits for b in range(bins)] * layers * channels)
+    cdf = cdf.to(DEV).to(torch.int16).reshape(layers, channels, bins)
+    out = torch.zeros((layers, max_sym, channels), dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(cdf, bs, lens, out)
+    torch.cuda.synchronize()
+    want = torch.tensor([s for s in range(max_sym) for _ in range(channels)] * layers, dtype=torch.uint8)
+    assert (want.reshape(layers, max_sym, channels).to(DEV) == out).all()
+
+
+def _kv_chunk_symbols(L=32, T=256, C=1024, seed=0):
+    """[2L, T, C] symbols of one K+V chunk: K layers 0-9 at 32 bins, later K
+    layers at 16; V layers at 16 (K stacked before V)."""
+    rng = np.random.default_rng(seed)
+    k = rng.normal(size=(L, T, C)).astype(np.float32)
+    v = rng.normal(size=(L, T, C)).astype(np.float32)
+    kb = np.where(np.arange(L) < 10, 32, 16)
+    return np.concatenate([oc.quantize(k, kb), oc.quantize(v, 16)], axis=0)
+
+
+def test_cachegen_kv_chunk_bit_exact(ops):
+    syms = _kv_chunk_symbols()
+    L2, T, C = syms.shape
+    nb = 32
+    d_syms = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d_syms, nb)
+    want_cdf = oc.calculate_cdf(syms, nb)
+    torch.cuda.synchronize()
+    assert np.array_equal(cdf.cpu().numpy(), want_cdf)
+    chunk = MAX_TOKENS_PER_CHUNK
+    out = torch.zeros((L2, C, chunk), dtype=torch.uint8, device=DEV)
+    lens = torch.zeros((L2, C), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, d_syms, out, lens)
+    want_out, want_len = oc.encode(want_cdf, syms, chunk)
+    torch.cuda.synchronize()
+    assert np.array_equal(lens.cpu().numpy(), want_len)
+    assert np.array_equal(out.cpu().numpy(), want_out)
+    assert want_len.max() <= chunk
+    stream, pref = oc.concat_streams(want_out, want_len)
+    dec = torch.zeros((L2, T, C), dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(cdf, torch.from_numpy(stream).to(DEV), torch.from_numpy(pref).to(DEV), dec)
+    torch.cuda.synchronize()
+    assert np.array_equal(dec.cpu().numpy(), syms)
+
+
+@pytest.mark.parametrize("n_tokens", [1, 20, 256])
+@pytest.mark.parametrize("n_layers", [1, 28])
+@pytest.mark.parametrize("num_heads", [1, 8])
+def test_encode_into_decode(ops, n_tokens, n_layers, num_heads):
+    """tests/v1/test_cachegen_kernels.py:242-345 (with this build's quantiser)."""
+    C = num_heads * 128
+    rng = np.random.default_rng(n_tokens * 31 + n_layers)
+    x = rng.normal(0, 2, size=(2 * n_layers, n_tokens, C)).astype(np.float32)
+    bins = np.where(np.arange(2 * n_layers) % n_layers < 10, 32, 16) if n_layers > 1 else 32
+    syms = oc.quantize(x, bins)
+    d = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d, 32)
+    out = torch.zeros((2 * n_layers, C, MAX_TOKENS_PER_CHUNK), dtype=torch.uint8, device=DEV)
+    lens = torch.zeros((2 * n_layers, C), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, d, out, lens)
+    torch.cuda.synchronize()
+    assert int(lens.max()) <= MAX_TOKENS_PER_CHUNK
+    stream, pref = oc.concat_streams(out.cpu().numpy(), lens.cpu().numpy())
+    dec = torch.zeros_like(d)
+    ops.decode_fast_prefsum(cdf, torch.from_numpy(stream).to(DEV), torch.from_numpy(pref).to(DEV), dec)
+    torch.cuda.synchronize()
+    assert torch.equal(dec, d)
+
+
+def test_edge_cases_vs_oracle(ops):
+    rng = np.random.default_rng(5)
+    L, T, C, nb = 3, 300, 96, 16
+    syms = rng.integers(0, nb, size=(L, T, C)).astype(np.uint8)
+    syms[0, :, :5] = 7                    # constant channels: one 1-bit code
+    syms[1, :, 10:20] = nb + 1            # out-of-range: not counted, not coded
+    syms[2] = np.minimum(syms[2], 1)      # two symbols
+    d = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d, nb)
+    want_cdf = oc.calculate_cdf(syms, nb)
+    torch.cuda.synchronize()
+    assert np.array_equal(cdf.cpu().numpy(), want_cdf)
+    chunk = 100                           # some streams overflow the row
+    guard = np.full((L, C, chunk), 0xEE, np.uint8)
+    out = torch.from_numpy(guard.copy()).to(DEV)
+    lens = torch.zeros((L, C), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, d, out, lens)
+    want_out, want_len = oc.encode(want_cdf, syms, chunk, out=guard.copy())
+    torch.cuda.synchronize()
+    assert np.array_equal(lens.cpu().numpy(), want_len)
+    assert np.array_equal(out.cpu().numpy(), want_out)
+    assert want_len.max() > chunk
+
+
+def test_single_bin_and_single_token(ops):
+    syms = np.zeros((2, 1, 32), np.uint8)
+    d = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d, 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(cdf.cpu().numpy(), oc.calculate_cdf(syms, 1))
+    out = torch.zeros((2, 32, 8), dtype=torch.uint8, device=DEV)
+    lens = torch.zeros((2, 32), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, d, out, lens)
+    torch.cuda.synchronize()
+    assert (lens.cpu() == 1).all()
+
+
+def test_decode_limits(ops):
+    cdf = torch.zeros((1, 48, 17), dtype=torch.int16, device=DEV)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        ops.decode_fast_prefsum(cdf, torch.zeros(4, dtype=torch.uint8, device=DEV),
+                                torch.zeros((1, 48), dtype=torch.int32, device=DEV),
+                                torch.zeros((1, 4, 48), dtype=torch.uint8, device=DEV))
+    cdf = torch.zeros((1, 32, 65), dtype=torch.int16, device=DEV)
+    with pytest.raises(RuntimeError, match="Max bins"):
+        ops.decode_fast_prefsum(cdf, torch.zeros(4, dtype=torch.uint8, device=DEV),
+                                torch.zeros((1, 32), dtype=torch.int32, device=DEV),
+                                torch.zeros((1, 4, 32), dtype=torch.uint8, device=DEV))
+    with pytest.raises(NotImplementedError):
+        ops.decode_fast_new(None, None, None, None)
