@@ -125,7 +125,7 @@ def cpu_baseline(budget_s=10.0):
 
 def load_traffic():
     """HBM traffic per launch from the committed rocprofv3 --pmc summary."""
-    path = os.path.join(REPO, "profiles", "kv_rows_copy_c2_traffic.json")
+    path = os.path.join(REPO, "profiles", "kv_rows_copy_llama8b_4096tok_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:

@@ -54,8 +54,10 @@ def test_blend_shape_4096_tokens(ops, neox):
     err = np.abs(got - want).max()
     assert err <= TOL, err
     assert np.count_nonzero(got != want) == 0
+    # one bf16 ulp of the exact value, plus the fp32 evaluation error, which
+    # dominates for outputs near zero (cancellation of O(1) terms)
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
-    assert (np.abs(got - exact) <= ulp).all()
+    assert (np.abs(got - exact) <= ulp + 1e-5).all()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
