@@ -132,6 +132,147 @@ def load_traffic():
         return json.load(f).get("traffic_bytes_per_launch")
 
 
+CG_LAYERS, CG_TOKENS, CG_CHANNELS, CG_CHUNK = 32, 256, 1024, 256
+
+
+def quantize_gpu(torch, x, bins):
+    """Per-(layer, channel) symmetric quantiser of [L, T, C] data into
+    [0, bins - 2] (bins per layer)."""
+    half = (bins // 2 - 1).to(torch.float32).view(-1, 1, 1)
+    amax = x.abs().amax(dim=1, keepdim=True).clamp_min(1e-30)
+    return (torch.round(x / amax * half) + half).to(torch.uint8)
+
+
+def bench_cachegen(torch, ops, dev, stream):
+    """calculate_cdf / encode / decode of one K+V chunk: 32 layers x 256
+    tokens x 1024 channels per K and V; K layers 0-9 quantised to 32 bins,
+    later K layers and all V layers to 16."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((2 * CG_LAYERS, CG_TOKENS, CG_CHANNELS), generator=g, device=dev)
+    bins = torch.full((2 * CG_LAYERS,), 16, device=dev)
+    bins[:10] = 32
+    sym = quantize_gpu(torch, x, bins)
+    cdf = ops.calculate_cdf(sym, 32)
+    out = torch.zeros((2 * CG_LAYERS, CG_CHANNELS, CG_CHUNK), dtype=torch.uint8, device=dev)
+    lens = torch.zeros((2 * CG_LAYERS, CG_CHANNELS), dtype=torch.int32, device=dev)
+    ops.encode_fast_new(cdf, sym, out, lens)
+    torch.cuda.synchronize()
+    rows = out.view(-1, CG_CHUNK)
+    keep = torch.arange(CG_CHUNK, device=dev)[None, :] < lens.view(-1, 1)
+    stream_bytes = rows[keep].contiguous()
+    pref = lens.view(-1).cumsum(0).to(torch.int32).view_as(lens)
+    dec = torch.empty_like(sym)
+    t_cdf = time_events(torch, stream, lambda: ops.calculate_cdf(sym, 32), 20)[0]
+    t_enc = time_events(torch, stream, lambda: ops.encode_fast_new(cdf, sym, out, lens), 20)[0]
+    t_dec = time_events(torch, stream, lambda: ops.decode_fast_prefsum(cdf, stream_bytes, pref, dec), 20)[0]
+    ok = bool(torch.equal(dec, sym))
+    n_sym = sym.numel()
+    enc_bytes = int(stream_bytes.numel())
+    cdf_bytes = cdf.numel() * 2
+    return {
+        "cachegen_calculate_cdf": {"ms": round(t_cdf, 4), "Gsym_per_s": round(n_sym / t_cdf / 1e6, 2),
+                                   "GBps": round((n_sym + cdf_bytes) / t_cdf / 1e6, 1)},
+        "cachegen_encode": {"ms": round(t_enc, 4), "Gsym_per_s": round(n_sym / t_enc / 1e6, 2),
+                            "GBps": round((n_sym + cdf_bytes + enc_bytes) / t_enc / 1e6, 1),
+                            "bits_per_symbol": round(8 * enc_bytes / n_sym, 3)},
+        "cachegen_decode": {"ms": round(t_dec, 4), "Gsym_per_s": round(n_sym / t_dec / 1e6, 2),
+                            "GBps": round((n_sym + cdf_bytes + enc_bytes) / t_dec / 1e6, 1),
+                            "round_trip_exact": ok},
+    }
+
+
+def bench_rope(torch, ops, dev, stream):
+    """rotary_embedding_k_fused: 4096 tokens x 8 heads x 128 bf16 K,
+    positions 0..4095 -> 1000..5095, theta 500000, neox."""
+    T, Hh, Dh, base = 4096, 8, 128, 500000.0
+    inv = 1.0 / (base ** (torch.arange(0, Dh, 2, dtype=torch.float32, device=dev) / Dh))
+    ang = torch.outer(torch.arange(8192, dtype=torch.float32, device=dev), inv)
+    cache = torch.cat((ang.cos(), ang.sin()), dim=-1).to(torch.bfloat16)
+    k = torch.randn((T, Hh * Dh), device=dev).to(torch.bfloat16)
+    old = torch.arange(T, device=dev)
+    new = old + 1000
+    t = time_events(torch, stream, lambda: ops.rotary_embedding_k_fused(old, new, k, Dh, cache, True), 20)[0]
+    nbytes = 2 * k.numel() * 2 + 2 * T * Dh * 2 + 16 * T
+    return {"rope_k_fused": {"ms": round(t, 4), "GBps": round(nbytes / t / 1e6, 1),
+                             "hbm_frac": round(nbytes / t / 1e6 / HBM_PEAK_GBS, 4),
+                             "tokens_per_s": round(T / t * 1e3)}}
+
+
+def bench_qwen32b_long_prefix(torch, ops, dev, stream):
+    """Qwen3-32B shape: 64 layers x 8x128 bf16, block 128; one 32768-token
+    request as 128 memory objects of 256 tokens; its 256 blocks drawn without
+    replacement from a 4096-block pool; 1638 slots (5%) set to -1 and
+    skipped.  Batched multi-layer store/retrieve, then
+    single_layer_kv_transfer layer by layer ([2, 32768, 1024] per layer)."""
+    L3, NB3, T3 = 64, 4096, 32768
+    torch.manual_seed(3)
+    flat = [torch.randn((NB3, BS, H, D), device=dev, dtype=torch.bfloat16) for _ in range(2 * L3)]
+    ptrs = torch.tensor([t.data_ptr() for t in flat], dtype=torch.int64, device=dev)
+    gen = torch.Generator().manual_seed(3)
+    blocks = torch.randperm(NB3, generator=gen)[: T3 // BS].tolist()
+    slots = torch.tensor(block_slots(blocks, BS, [T3]), dtype=torch.int64)
+    pad = torch.randperm(T3, generator=gen)[: round(0.05 * T3)]
+    slots[pad] = -1
+    valid = int((slots >= 0).sum())
+    slots = slots.to(dev)
+    starts = list(range(0, T3, CHUNK))
+    chunks = [torch.empty((2, L3, CHUNK, W), dtype=torch.bfloat16, device=dev) for _ in starts]
+    pbs3 = NB3 * BS
+    store = lambda: ops.multi_layer_kv_transfer_batched(chunks, ptrs, slots, starts, dev, pbs3, True, False, 2, W, W, 0)
+    retr = lambda: ops.multi_layer_kv_transfer_batched(chunks, ptrs, slots, starts, dev, pbs3, False, False, 2, W, W, 0)
+    store(); retr()
+    t_s = time_events(torch, stream, store, 5)[0]
+    t_r = time_events(torch, stream, retr, 5)[0]
+    buf = torch.empty((2, T3, W), dtype=torch.bfloat16, device=dev)
+
+    def sl(direction):
+        for l in range(L3):
+            ops.single_layer_kv_transfer(buf, (flat[2 * l], flat[2 * l + 1]), slots, direction, 2)
+
+    sl(True); sl(False)
+    t_ss = time_events(torch, stream, lambda: sl(True), 3)[0]
+    t_sr = time_events(torch, stream, lambda: sl(False), 3)[0]
+    P3 = L3 * valid * 2 * W * ES
+    out = {}
+    for name, t in (("qwen32b_multi_layer_store", t_s), ("qwen32b_multi_layer_retrieve", t_r),
+                    ("qwen32b_single_layer_store_64_layers", t_ss), ("qwen32b_single_layer_retrieve_64_layers", t_sr)):
+        out[name] = {"ms": round(t, 3), "payload_GBps": round(P3 / t / 1e6, 1),
+                     "hbm_frac": round(2 * P3 / t / 1e6 / HBM_PEAK_GBS, 4)}
+    out["qwen32b_valid_tokens"] = valid
+    del flat, chunks, buf
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_mla_576(torch, ops, dev, stream):
+    """DeepSeek-V3-style latent cache: 61 layers, one [1024, 64, 576] bf16
+    tensor per layer (use_mla=True), N(0, 0.5); 8 requests x 2048 tokens in
+    a random block permutation; memory objects [1, 61, 2048, 576]."""
+    L4, NB4, BS4, W4, NR, TR = 61, 1024, 64, 576, 8, 2048
+    torch.manual_seed(4)
+    caches = [torch.randn((NB4, BS4, W4), device=dev, dtype=torch.bfloat16) * 0.5 for _ in range(L4)]
+    ptrs = torch.tensor([t.data_ptr() for t in caches], dtype=torch.int64, device=dev)
+    gen = torch.Generator().manual_seed(4)
+    blocks = torch.randperm(NB4, generator=gen).tolist()
+    slots = torch.tensor(block_slots(blocks, BS4, [TR] * NR), dtype=torch.int64, device=dev)
+    starts = [i * TR for i in range(NR)]
+    objs = [torch.empty((1, L4, TR, W4), dtype=torch.bfloat16, device=dev) for _ in range(NR)]
+    pbs4 = NB4 * BS4
+    store = lambda: ops.multi_layer_kv_transfer_batched(objs, ptrs, slots, starts, dev, pbs4, True, True, 1, 0, 0, 0)
+    retr = lambda: ops.multi_layer_kv_transfer_batched(objs, ptrs, slots, starts, dev, pbs4, False, True, 1, 0, 0, 0)
+    store(); retr()
+    t_s = time_events(torch, stream, store, 10)[0]
+    t_r = time_events(torch, stream, retr, 10)[0]
+    P4 = L4 * NR * TR * W4 * ES
+    out = {}
+    for name, t in (("mla576_store", t_s), ("mla576_retrieve", t_r)):
+        out[name] = {"ms": round(t, 4), "payload_GBps": round(P4 / t / 1e6, 1),
+                     "hbm_frac": round(2 * P4 / t / 1e6 / HBM_PEAK_GBS, 4)}
+    del caches, objs
+    torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,7 +280,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,pinned,staged,memcpy",
+    ap.add_argument("--modes", default="d2d,per_chunk,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -172,27 +313,25 @@ def main(argv=None):
         retrieve()
     torch.cuda.synchronize()
 
-    # Timed region: exactly `steps` store+retrieve steps, with HIP events
-    # around every launch on the launch stream.
-    ev = []
+    # Timed region: exactly `steps` store+retrieve steps between two HIP
+    # events on the launch stream; the only kernels in it are the 2 * steps
+    # gather/scatter launches, so the event time over 2 * steps is the
+    # kernel's average launch duration (inter-launch gaps included).
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record(stream)
     for _ in range(args.steps):
-        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-        a.record(stream)
         store()
-        b.record(stream)
         retrieve()
-        c.record(stream)
-        ev.append((a, b, c))
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    store_ms = [a.elapsed_time(b) for a, b, _ in ev]
-    retr_ms = [b.elapsed_time(c) for _, b, c in ev]
+    gpu_ms = e0.elapsed_time(e1)
     step_ms = wall * 1e3 / args.steps
     value = 2 * payload * args.steps / wall / 1e9
-
-    kern_avg_ms = (statistics.mean(store_ms) + statistics.mean(retr_ms)) / 2
+    kern_avg_ms = gpu_ms / (2 * args.steps)
     achieved = 2 * payload / (kern_avg_ms * 1e-3) / 1e9   # HBM bytes (read + write) per launch
     roofline = {
         "bound": "hbm",
@@ -202,8 +341,12 @@ def main(argv=None):
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": load_traffic(),
     }
+    # Per-direction split (outside the timed region).
+    store_ms = time_events(torch, stream, store, 10)[2]
+    retr_ms = time_events(torch, stream, retrieve, 10)[2]
 
     extra = {}
+    extra_cg, extra_rope = {}, {}
     if "per_chunk" in sel:
         # Per-chunk drop-in call path (one multi_layer_kv_transfer per chunk).
         def store_per_chunk():
@@ -263,6 +406,23 @@ def main(argv=None):
         extra["hipmemcpy_d2h_pinned"] = time_events(
             torch, stream, lambda: host_big.copy_(big_a, non_blocking=True), 5)[0]
 
+    if "cachegen" in sel:
+        extra_cg = bench_cachegen(torch, ops, dev, stream)
+    if "rope" in sel:
+        extra_rope = bench_rope(torch, ops, dev, stream)
+
+    extra_big = {}
+    if "qwen32b" in sel or "mla576" in sel:
+        # Free the Llama-shape pool before the larger configurations.
+        del flat, chunks
+        if "pinned" in sel or "staged" in sel:
+            del host_chunks
+        torch.cuda.empty_cache()
+    if "qwen32b" in sel:
+        extra_big.update(bench_qwen32b_long_prefix(torch, ops, dev, stream))
+    if "mla576" in sel:
+        extra_big.update(bench_mla_576(torch, ops, dev, stream))
+
     def gbs(nbytes, ms):
         return round(nbytes / (ms * 1e-3) / 1e9, 2)
 
@@ -282,6 +442,9 @@ def main(argv=None):
         if name.startswith("pinned") or name in ("hipmemcpy_h2d_pinned", "hipmemcpy_d2h_pinned"):
             entry["pcie_frac"] = round(payload / (ms * 1e-3) / 1e9 / PCIE_PEAK_GBS, 4)
         modes[name] = entry
+    modes.update(extra_cg)
+    modes.update(extra_rope)
+    modes.update(extra_big)
 
     out = {
         "metric": METRIC,

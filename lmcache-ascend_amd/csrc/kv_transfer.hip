@@ -38,12 +38,36 @@
 
 namespace lmc {
 
+// Launch geometry (compile-time; the defaults are the measured best on
+// MI355X for 2 KiB rows).
+#ifndef LMC_KV_THREADS
+#define LMC_KV_THREADS 256        // threads per block
+#endif
+#ifndef LMC_KV_ROWS_PER_WAVE
+#define LMC_KV_ROWS_PER_WAVE 1    // work items a wave moves per pass
+#endif
+#ifndef LMC_KV_SEGS
+#define LMC_KV_SEGS 2             // 64-lane accesses per work item
+#endif
+#ifndef LMC_KV_XCD_REMAP
+#define LMC_KV_XCD_REMAP 0        // give each XCD a contiguous block range
+#endif
+#ifndef LMC_KV_GRID_CAP
+#define LMC_KV_GRID_CAP 65535     // blocks per chunk (grid-stride beyond)
+#endif
+#ifndef LMC_KV_NT_LOADS
+#define LMC_KV_NT_LOADS 1         // streaming hint on loads of HBM copies
+#endif
+#ifndef LMC_KV_NT_STORES
+#define LMC_KV_NT_STORES 1        // streaming hint on stores of HBM copies
+#endif
+
 constexpr int kMaxPlanes = 3;
 constexpr int kMaxChunks = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = LMC_KV_THREADS;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowsPerWave = 2;
-constexpr int kSegs = 2;
+constexpr int kRowsPerWave = LMC_KV_ROWS_PER_WAVE;
+constexpr int kSegs = LMC_KV_SEGS;
 
 // Byte geometry of one plane (K, V or DSA) of a copy.
 struct PlaneDesc {
@@ -76,7 +100,7 @@ struct CopyJob {
   int32_t block_size;          // 0: flat rows
   int64_t num_slots;           // valid slots are [0, num_slots)
   int32_t page2lmc;            // 1: paged -> LMC (store), 0: LMC -> paged
-  int32_t pad_;
+  int32_t slices_per_row;      // work items per row (widest plane)
 };
 
 struct ChunkList {
@@ -96,11 +120,11 @@ template <> struct VecOf<2> { using T = uint16_t; };
 template <> struct VecOf<1> { using T = uint8_t; };
 
 template <typename T, bool NT> __device__ __forceinline__ T ld(const T *p) {
-  if constexpr (NT) return __builtin_nontemporal_load(p);
+  if constexpr (NT && LMC_KV_NT_LOADS) return __builtin_nontemporal_load(p);
   else return *p;
 }
 template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
-  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  if constexpr (NT && LMC_KV_NT_STORES) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
 
@@ -161,68 +185,81 @@ __device__ __forceinline__ int64_t row_ptrs(const CopyJob &job, uint8_t *lmc,
   return pd.row_bytes;
 }
 
+// One work item is a slice of one row: kSegs 64-lane accesses of VEC bytes
+// (2 KiB with 16-byte accesses, a whole row at the Llama-3-8B shape).  A
+// wave owns kRowsPerWave items per pass: it resolves their addresses with
+// scalar work, issues every load, then every store.
 template <int VEC, bool NT>
 __global__ void __launch_bounds__(kThreads)
     kv_rows_copy(const CopyJob job, const ChunkList chunks) {
   using V = typename VecOf<VEC>::T;
+  constexpr int kSlice = 64 * VEC * kSegs;
   const int c = blockIdx.y;
   const int tok0 = chunks.tok_start[c];
   const int T = chunks.tok_count[c];
   const int per_plane = job.n_layers * T;
-  const int rows = job.n_planes * per_plane;
+  const int spr = job.slices_per_row;
+  const int items = job.n_planes * per_plane * spr;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t *lmc = reinterpret_cast<uint8_t *>(chunks.lmc[c]);
+  int bx = blockIdx.x;
+#if LMC_KV_XCD_REMAP
+  // Blocks are dispatched round-robin over the 8 XCDs; map each XCD's
+  // blocks onto one contiguous range of work.
+  if ((gridDim.x & 7) == 0) bx = (bx & 7) * (gridDim.x >> 3) + (bx >> 3);
+#endif
   const int step = gridDim.x * kWaves * kRowsPerWave;
 
-  for (int r0 = (blockIdx.x * kWaves + wave) * kRowsPerWave; r0 < rows;
-       r0 += step) {
+  for (int i0 = (bx * kWaves + wave) * kRowsPerWave; i0 < items; i0 += step) {
     const uint8_t *src[kRowsPerWave];
     uint8_t *dst[kRowsPerWave];
-    int64_t nb[kRowsPerWave];
-    int64_t nb_max = 0;
+    int64_t nb[kRowsPerWave], off0[kRowsPerWave];
     bool slow = false;
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
       nb[r] = 0;
+      off0[r] = 0;
       src[r] = nullptr;
       dst[r] = nullptr;
-      if (r0 + r < rows)
-        nb[r] = row_ptrs(job, lmc, tok0, T, per_plane, r0 + r, src[r], dst[r]);
+      const int item = i0 + r;
+      if (item < items) {
+        const int row = item / spr;
+        off0[r] = static_cast<int64_t>(item - row * spr) * kSlice;
+        nb[r] = row_ptrs(job, lmc, tok0, T, per_plane, row, src[r], dst[r]);
+      }
       // The host checked every alignment it can see; a table entry (a device
-      // value) that is not VEC-aligned sends the row to the byte path.
-      if (nb[r] > 0 &&
+      // value) that is not VEC-aligned sends the item to the byte path.
+      if (nb[r] > off0[r] &&
           ((reinterpret_cast<uintptr_t>(src[r]) |
             reinterpret_cast<uintptr_t>(dst[r])) &
            (VEC - 1)) != 0) {
         slow = true;
       }
-      nb_max = nb[r] > nb_max ? nb[r] : nb_max;
     }
     if (slow) {
 #pragma unroll
-      for (int r = 0; r < kRowsPerWave; ++r)
-        for (int64_t o = lane; o < nb[r]; o += 64) dst[r][o] = src[r][o];
+      for (int r = 0; r < kRowsPerWave; ++r) {
+        const int64_t end = nb[r] < off0[r] + kSlice ? nb[r] : off0[r] + kSlice;
+        for (int64_t o = off0[r] + lane; o < end; o += 64) dst[r][o] = src[r][o];
+      }
       continue;
     }
-    for (int64_t base = 0; base < nb_max; base += 64 * VEC * kSegs) {
-      V v[kRowsPerWave][kSegs];
+    V v[kRowsPerWave][kSegs];
 #pragma unroll
-      for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
-        for (int s = 0; s < kSegs; ++s) {
-          const int64_t o = base + (s * 64 + lane) * VEC;
-          if (o < nb[r])
-            v[r][s] = ld<V, NT>(reinterpret_cast<const V *>(src[r] + o));
-        }
+      for (int s = 0; s < kSegs; ++s) {
+        const int64_t o = off0[r] + (s * 64 + lane) * VEC;
+        if (o < nb[r]) v[r][s] = ld<V, NT>(reinterpret_cast<const V *>(src[r] + o));
+      }
 #pragma unroll
-      for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
-        for (int s = 0; s < kSegs; ++s) {
-          const int64_t o = base + (s * 64 + lane) * VEC;
-          if (o < nb[r]) st<V, NT>(reinterpret_cast<V *>(dst[r] + o), v[r][s]);
-        }
-    }
+      for (int s = 0; s < kSegs; ++s) {
+        const int64_t o = off0[r] + (s * 64 + lane) * VEC;
+        if (o < nb[r]) st<V, NT>(reinterpret_cast<V *>(dst[r] + o), v[r][s]);
+      }
   }
 }
 
@@ -272,11 +309,19 @@ int pick_vec(const CopyJob &job, const ChunkList &chunks, int n_chunks) {
 }
 
 template <int VEC>
-void launch_vec(const CopyJob &job, const ChunkList &chunks, int n_chunks,
+void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
                 int max_rows, bool nt, hipStream_t stream) {
-  const int rows_per_block = kWaves * kRowsPerWave;
-  int gx = (max_rows + rows_per_block - 1) / rows_per_block;
-  gx = std::max(1, std::min(gx, 65535));
+  CopyJob job = job_in;
+  constexpr int64_t kSlice = 64 * VEC * kSegs;
+  int64_t widest = 0;
+  for (int p = 0; p < job.n_planes; ++p)
+    widest = std::max(widest, job.plane[p].row_bytes);
+  job.slices_per_row = static_cast<int32_t>(std::max<int64_t>(1, (widest + kSlice - 1) / kSlice));
+  const int64_t max_items = static_cast<int64_t>(max_rows) * job.slices_per_row;
+  check(max_items < (int64_t(1) << 31), "too many work items in one chunk");
+  const int items_per_block = kWaves * kRowsPerWave;
+  int gx = static_cast<int>((max_items + items_per_block - 1) / items_per_block);
+  gx = std::max(1, std::min(gx, LMC_KV_GRID_CAP));
   dim3 grid(gx, n_chunks), block(kThreads);
   if (nt)
     hipLaunchKernelGGL((kv_rows_copy<VEC, true>), grid, block, 0, stream, job,

@@ -5,7 +5,8 @@
 // is HBM-bound elementwise work (each key element is read and written once;
 // the cos/sin rows of the two positions are shared by all heads of a token
 // and stay in L2), so there is no tiling: one thread owns VP consecutive
-// rotation pairs of one (token, head) and moves them with vector loads.
+// rotation pairs of one (token, head) and moves them with vector loads of up
+// to 16 bytes (VP = 8 for bf16/fp16 neox).
 //
 // Arithmetic: the key and the cos/sin values are widened to fp32; the
 // inverse rotation by the old angle and the forward rotation by the new one
@@ -176,6 +177,7 @@ void launch(const RopeArgs &a, hipStream_t s) {
 template <typename KD, typename CD, bool NEOX>
 void launch_vp(const RopeArgs &a, int vp, hipStream_t s) {
   switch (vp) {
+  case 8: launch<KD, CD, NEOX, 8>(a, s); break;
   case 4: launch<KD, CD, NEOX, 4>(a, s); break;
   case 2: launch<KD, CD, NEOX, 2>(a, s); break;
   default: launch<KD, CD, NEOX, 1>(a, s); break;
@@ -271,7 +273,7 @@ extern "C" int lmc_rotary_embedding_k_fused(const lmc_tensor *old_positions,
              ok(reinterpret_cast<uintptr_t>(a.cache), cvec) &&
              ok(rot * ces, cvec) && ok(half * ces, cvec);
     };
-    const int vp = aligned(4) ? 4 : aligned(2) ? 2 : 1;
+    const int vp = aligned(8) ? 8 : aligned(4) ? 4 : aligned(2) ? 2 : 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (k.dtype) {
     case LMC_BF16: launch_cache<BF16>(a, c.dtype, is_neox != 0, vp, s); break;

@@ -10,7 +10,11 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblmcache_amd.so")
+# LMCACHE_AMD_LIB selects another build of the library (for example one
+# compiled with different launch geometry).
+LIB_PATH = os.environ.get("LMCACHE_AMD_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "liblmcache_amd.so"
+)
 
 MAX_DIMS = 6
 

@@ -51,32 +51,28 @@ class GPUKVFormat(IntEnum):
     NL_X_NB_TWO_NH_BS_HS = 7
 
 
+_DIMS = ctypes.c_int64 * _lib.MAX_DIMS
+
+
 def _desc(t: torch.Tensor) -> _lib.LmcTensor:
-    if not isinstance(t, torch.Tensor):
-        raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}")
-    d = _lib.LmcTensor()
-    d.data = t.data_ptr()
+    """lmc_tensor descriptor of a tensor (pointer, dtype, device, geometry)."""
     try:
-        d.dtype = _DTYPES[t.dtype]
+        dt = _DTYPES[t.dtype]
     except KeyError:
         raise RuntimeError(f"ScalarType not supported: {t.dtype}") from None
-    dev = t.device
-    if dev.type == "cuda":
-        d.device = dev.index if dev.index is not None else torch.cuda.current_device()
-    elif dev.type == "cpu":
-        d.device = -1
+    except AttributeError:
+        raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}") from None
+    if t.is_cuda:
+        idx = t.device.index
+        dev = idx if idx is not None else torch.cuda.current_device()
+    elif t.device.type == "cpu":
+        dev = -1
     else:
-        raise RuntimeError(
-            "Invalid device. Device must be a GPU or pinned cpu."
-        )
+        raise RuntimeError("Invalid device. Device must be a GPU or pinned cpu.")
     n = t.dim()
     if n > _lib.MAX_DIMS:
         raise RuntimeError(f"tensors of more than {_lib.MAX_DIMS} dims are not supported")
-    d.ndim = n
-    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
-        d.sizes[i] = s
-        d.strides[i] = st
-    return d
+    return _lib.LmcTensor(t.data_ptr(), dt, dev, n, 0, _DIMS(*t.shape), _DIMS(*t.stride()))
 
 
 def _ref(d: _lib.LmcTensor):
