@@ -263,6 +263,121 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Tile kernel.  A wave owns a tile of up to 64 consecutive tokens of one
+// (plane, layer) of a chunk.  Lane i resolves row i once (slot load, range
+// check, paged and LMC addresses); the tile's bytes are then streamed as one
+// flattened range of VEC-byte vectors, kTileU accesses in flight per lane,
+// each lane fetching its row's addresses from the owning lane with a
+// cross-lane shuffle.  The scalar work per tile (pointer-table entry, plane
+// geometry) and the slot loads are amortised over the whole tile, and every
+// access is full whatever the row width.
+#ifndef LMC_KV_TILE_U
+#define LMC_KV_TILE_U 4           // accesses in flight per lane
+#endif
+constexpr int kTileU = LMC_KV_TILE_U;
+
+__device__ __forceinline__ uint64_t shfl64(uint64_t x, int src_lane) {
+  const int lo = __shfl(static_cast<int>(x), src_lane, 64);
+  const int hi = __shfl(static_cast<int>(x >> 32), src_lane, 64);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+         static_cast<uint32_t>(lo);
+}
+
+template <int VEC, bool NT>
+__global__ void __launch_bounds__(kThreads)
+    kv_tiles_copy(const CopyJob job, const ChunkList chunks, int tile_rows) {
+  using V = typename VecOf<VEC>::T;
+  const int c = blockIdx.y;
+  const int tok0 = chunks.tok_start[c];
+  const int T = chunks.tok_count[c];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t *lmc = reinterpret_cast<uint8_t *>(chunks.lmc[c]);
+  const int tiles_per_pl = (T + tile_rows - 1) / tile_rows;
+  const int n_tiles = job.n_planes * job.n_layers * tiles_per_pl;
+  for (int tile = blockIdx.x * kWaves + wave; tile < n_tiles;
+       tile += gridDim.x * kWaves) {
+    const int pl = tile / tiles_per_pl;
+    const int t0 = (tile - pl * tiles_per_pl) * tile_rows;
+    const int p = pl / job.n_layers;
+    const int l = pl - p * job.n_layers;
+    const int nrows = T - t0 < tile_rows ? T - t0 : tile_rows;
+    const PlaneDesc &pd = job.plane[p];
+    uint64_t pbase;
+    if (job.table != nullptr) {
+      pbase = job.table[static_cast<int64_t>(l) * job.table_ppl + job.table_idx[p]];
+      pbase = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(pbase))) |
+              (static_cast<uint64_t>(static_cast<uint32_t>(
+                   __builtin_amdgcn_readfirstlane(static_cast<int>(pbase >> 32))))
+               << 32);
+    } else {
+      pbase = job.base[p];
+    }
+    uint8_t *lm_base = lmc + pd.lmc_off_fixed + pd.lmc_off_per_t * T +
+                       static_cast<int64_t>(l) * (pd.lmc_layer_fixed + pd.lmc_layer_per_t * T);
+    // Row setup: lane i owns row t0 + i.  A skipped slot leaves src == 0.
+    uint64_t my_src = 0, my_dst = 0;
+    if (lane < nrows) {
+      const int t = t0 + lane;
+      const int64_t slot = job.slot_i32
+                               ? static_cast<int64_t>(static_cast<const int32_t *>(job.slots)[tok0 + t])
+                               : static_cast<const int64_t *>(job.slots)[tok0 + t];
+      if (slot >= 0 && slot < job.num_slots) {
+        int64_t poff = pd.paged_off;
+        if (job.block_size > 0) {
+          const uint32_t s32 = static_cast<uint32_t>(slot);
+          const uint32_t bs = static_cast<uint32_t>(job.block_size);
+          const uint32_t blk = s32 / bs;
+          poff += static_cast<int64_t>(blk) * pd.blk_stride +
+                  static_cast<int64_t>(s32 - blk * bs) * pd.row_pitch;
+        } else {
+          poff += slot * pd.row_pitch;
+        }
+        const uint64_t paged = pbase + static_cast<uint64_t>(poff);
+        const uint64_t lm = reinterpret_cast<uint64_t>(lm_base) +
+                            static_cast<uint64_t>(static_cast<int64_t>(t) * pd.lmc_token_stride);
+        my_src = job.page2lmc ? paged : lm;
+        my_dst = job.page2lmc ? lm : paged;
+      }
+    }
+    const int vpr = static_cast<int>(pd.row_bytes / VEC);
+    const int total = nrows * vpr;
+    // Any misaligned row (a misaligned table entry) sends the tile to the
+    // byte path.
+    const bool slow = __any(((my_src | my_dst) & (VEC - 1)) != 0);
+    if (slow) {
+      for (int r = 0; r < nrows; ++r) {
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(shfl64(my_src, r));
+        uint8_t *dst = reinterpret_cast<uint8_t *>(shfl64(my_dst, r));
+        if (src != nullptr)
+          for (int64_t o = lane; o < pd.row_bytes; o += 64) dst[o] = src[o];
+      }
+      continue;
+    }
+    for (int f0 = 0; f0 < total; f0 += 64 * kTileU) {
+      V v[kTileU];
+      uint64_t dst[kTileU];
+      bool live[kTileU];
+#pragma unroll
+      for (int u = 0; u < kTileU; ++u) {
+        const int f = f0 + u * 64 + lane;
+        const int r = f / vpr;
+        const int col = f - r * vpr;
+        const int src_lane = r < 64 ? r : 63;
+        const uint64_t src = shfl64(my_src, src_lane);
+        dst[u] = shfl64(my_dst, src_lane);
+        live[u] = f < total && src != 0;
+        if (live[u])
+          v[u] = ld<V, NT>(reinterpret_cast<const V *>(src + static_cast<uint64_t>(col) * VEC));
+        dst[u] += static_cast<uint64_t>(col) * VEC;
+      }
+#pragma unroll
+      for (int u = 0; u < kTileU; ++u)
+        if (live[u]) st<V, NT>(reinterpret_cast<V *>(dst[u]), v[u]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -317,19 +432,40 @@ void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
   for (int p = 0; p < job.n_planes; ++p)
     widest = std::max(widest, job.plane[p].row_bytes);
   job.slices_per_row = static_cast<int32_t>(std::max<int64_t>(1, (widest + kSlice - 1) / kSlice));
-  const int64_t max_items = static_cast<int64_t>(max_rows) * job.slices_per_row;
-  check(max_items < (int64_t(1) << 31), "too many work items in one chunk");
-  const int items_per_block = kWaves * kRowsPerWave;
-  int gx = static_cast<int>((max_items + items_per_block - 1) / items_per_block);
-  gx = std::max(1, std::min(gx, LMC_KV_GRID_CAP));
-  dim3 grid(gx, n_chunks), block(kThreads);
-  if (nt)
-    hipLaunchKernelGGL((kv_rows_copy<VEC, true>), grid, block, 0, stream, job,
-                       chunks);
-  else
-    hipLaunchKernelGGL((kv_rows_copy<VEC, false>), grid, block, 0, stream, job,
-                       chunks);
+  bool whole_slices = true;
+  for (int p = 0; p < job.n_planes; ++p)
+    whole_slices = whole_slices && job.plane[p].row_bytes % kSlice == 0;
+  dim3 block(kThreads);
+  if (whole_slices) {
+    // Every row is a whole number of slices: one slice per wave.
+    const int64_t max_items = static_cast<int64_t>(max_rows) * job.slices_per_row;
+    check(max_items < (int64_t(1) << 31), "too many work items in one chunk");
+    const int items_per_block = kWaves * kRowsPerWave;
+    int gx = static_cast<int>((max_items + items_per_block - 1) / items_per_block);
+    dim3 grid(std::max(1, std::min(gx, LMC_KV_GRID_CAP)), n_chunks);
+    if (nt)
+      hipLaunchKernelGGL((kv_rows_copy<VEC, true>), grid, block, 0, stream, job, chunks);
+    else
+      hipLaunchKernelGGL((kv_rows_copy<VEC, false>), grid, block, 0, stream, job, chunks);
+  } else {
+    // Narrower or odd rows: tiles of about 32 KiB of the widest plane,
+    // 16..64 rows.
+    const int tile_rows = static_cast<int>(
+        std::max<int64_t>(16, std::min<int64_t>(64, 32768 / std::max<int64_t>(1, widest))));
+    const int64_t max_tokens = max_rows / (job.n_planes * job.n_layers);
+    const int64_t tiles = static_cast<int64_t>(job.n_planes) * job.n_layers *
+                          ((max_tokens + tile_rows - 1) / tile_rows);
+    check(widest / VEC * tile_rows < (int64_t(1) << 31) && tiles < (int64_t(1) << 31),
+          "too many tiles in one chunk");
+    int gx = static_cast<int>((tiles + kWaves - 1) / kWaves);
+    dim3 grid(std::max(1, std::min(gx, LMC_KV_GRID_CAP)), n_chunks);
+    if (nt)
+      hipLaunchKernelGGL((kv_tiles_copy<VEC, true>), grid, block, 0, stream, job, chunks, tile_rows);
+    else
+      hipLaunchKernelGGL((kv_tiles_copy<VEC, false>), grid, block, 0, stream, job, chunks, tile_rows);
+  }
 }
+
 
 bool nontemporal_enabled() {
   static const bool on = [] {

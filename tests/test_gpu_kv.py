@@ -128,6 +128,36 @@ def test_multi_layer_store_retrieve_vs_oracle(ops, fmt, num_tokens, chunk, num_l
             assert np.array_equal(to_bytes(z), zn)
 
 
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("num_heads,head_size", [(8, 256), (1, 256), (4, 128)])
+def test_multi_layer_row_widths(ops, fmt, num_heads, head_size):
+    """tests/v1/test_mem_kernels.py:24-284 use head_size 256: 4 KiB rows
+    (two slices per row); 1 head gives 512-byte rows (tiles)."""
+    gen = torch.Generator().manual_seed(fmt * 100 + num_heads + head_size)
+    L, NB, BS, T = 4, 64, 128, 500
+    W = num_heads * head_size
+    pbs = NB * BS
+    layers = _paged(fmt, L, NB, BS, num_heads, head_size, gen)
+    flat = _flat_tensors(layers)
+    slots = torch.tensor(sample_slots(pbs, T, seed=7), dtype=torch.int64)
+    table_np = [to_bytes(t) for t in flat]
+    lmc = torch.zeros((2, L, T, W), dtype=torch.bfloat16, device=DEV)
+    ops.multi_layer_kv_transfer(lmc, ptr_table(flat, DEV), slots.to(DEV), torch.device(DEV), pbs, True, False, fmt,
+                                W, W, 0)
+    want = np.zeros(2 * L * T * W * 2, np.uint8)
+    ok.multi_layer_kv_transfer(want, table_np, slots.numpy(), pbs, True, False, fmt, L, W, 2)
+    _sync()
+    assert np.array_equal(to_bytes(lmc), want)
+    zero = [torch.zeros_like(t) for t in flat]
+    ops.multi_layer_kv_transfer(lmc, ptr_table(zero, DEV), slots.to(DEV), torch.device(DEV), pbs, False, False, fmt,
+                                W, W, 0)
+    zero_np = [np.zeros_like(x) for x in table_np]
+    ok.multi_layer_kv_transfer(want, zero_np, slots.numpy(), pbs, False, False, fmt, L, W, 2)
+    _sync()
+    for z, zn in zip(zero, zero_np):
+        assert np.array_equal(to_bytes(z), zn)
+
+
 def test_multi_layer_equals_load_and_reshape_flash(ops):
     """tests/v1/test_mem_kernels.py:24-168: multi_layer (MERGED) equals the
     layer-by-layer load_and_reshape_flash result, and the retrieve restores
