@@ -280,7 +280,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
+    ap.add_argument("--modes", default="d2d,per_chunk,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -395,6 +395,18 @@ def main(argv=None):
         extra["pinned_staged_store"] = time_events(torch, stream, store_fused, 5)[0]
         extra["pinned_staged_retrieve"] = time_events(torch, stream, retrieve_fused, 5)[0]
 
+    if "contiguous" in sel:
+        # The same kernel and bytes with slots 0..4095 (consecutive blocks):
+        # a contiguous copy, the ceiling the scattered-slot case is judged by.
+        lin = torch.arange(n_tok, dtype=torch.int64, device=dev)
+        c_store = lambda: ops.multi_layer_kv_transfer_batched(chunks, ptrs, lin, starts, dev, pbs, True, False, 2,
+                                                               W, W, 0)
+        c_retr = lambda: ops.multi_layer_kv_transfer_batched(chunks, ptrs, lin, starts, dev, pbs, False, False, 2,
+                                                              W, W, 0)
+        c_store(); c_retr()
+        extra["d2d_contiguous_slots_store"] = time_events(torch, stream, c_store, 10)[0]
+        extra["d2d_contiguous_slots_retrieve"] = time_events(torch, stream, c_retr, 10)[0]
+
     if "memcpy" in sel:
         # Reference copies: hipMemcpy D2D of the same byte count, pinned H2D/D2H.
         big_a = torch.empty(payload, dtype=torch.uint8, device=dev)
@@ -436,6 +448,9 @@ def main(argv=None):
     for name, ms in extra.items():
         entry = {"ms": round(ms, 4)}
         if name.startswith("hipmemcpy_d2d"):
+            entry["hbm_GBps"] = gbs(2 * payload, ms)
+        elif name.startswith("d2d_"):
+            entry["payload_GBps"] = gbs(payload, ms)
             entry["hbm_GBps"] = gbs(2 * payload, ms)
         else:
             entry["payload_GBps"] = gbs(payload, ms)
