@@ -280,7 +280,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
+    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -346,7 +346,7 @@ def main(argv=None):
     retr_ms = time_events(torch, stream, retrieve, 10)[2]
 
     extra = {}
-    extra_cg, extra_rope = {}, {}
+    extra_cg, extra_rope, extra_calls = {}, {}, {}
     if "per_chunk" in sel:
         # Per-chunk drop-in call path (one multi_layer_kv_transfer per chunk).
         def store_per_chunk():
@@ -359,6 +359,26 @@ def main(argv=None):
 
         extra["d2d_per_chunk_calls_store"] = time_events(torch, stream, store_per_chunk, 10)[0]
         extra["d2d_per_chunk_calls_retrieve"] = time_events(torch, stream, retrieve_per_chunk, 10)[0]
+
+    if "call_overhead" in sel:
+        # Host time per drop-in call on a 1-token transfer, through the C++
+        # binding and through ctypes (wall clock per call, stream not drained).
+        one = slots[:1]
+        tiny = torch.empty((2, L, 1, W), dtype=torch.bfloat16, device=dev)
+        paths = {"binding": ops.multi_layer_kv_transfer, "ctypes": ops._multi_layer_kv_transfer_ctypes}
+        for name, fn in paths.items():
+            if name == "binding" and getattr(ops, "_ext", None) is None:
+                continue
+            for _ in range(50):
+                fn(tiny, ptrs, one, dev, pbs, True, False, 2, W, W, 0)
+            torch.cuda.synchronize()
+            n_calls = 2000
+            t0 = time.perf_counter()
+            for _ in range(n_calls):
+                fn(tiny, ptrs, one, dev, pbs, True, False, 2, W, W, 0)
+            host_us = (time.perf_counter() - t0) / n_calls * 1e6
+            torch.cuda.synchronize()
+            extra_calls[f"host_us_per_call_{name}"] = round(host_us, 2)
 
     if "pinned" in sel or "staged" in sel:
         # Memory objects in page-locked host memory.
@@ -460,6 +480,7 @@ def main(argv=None):
     modes.update(extra_cg)
     modes.update(extra_rope)
     modes.update(extra_big)
+    modes.update(extra_calls)
 
     out = {
         "metric": METRIC,

@@ -58,6 +58,38 @@ def _compile(src: str) -> str:
     return obj
 
 
+EXT_SRC = "torch_binding.cpp"
+
+
+def build_torch_binding(verbose: bool = False) -> str:
+    """Compiles the pybind11 binding (host code only, g++) against torch."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    suffix = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(HERE, "lmcache_amd", "_c_ops_ext" + suffix)
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    incs = ce.include_paths() + [sysconfig.get_paths()["include"], os.path.join(rocm, "include"),
+                                 os.path.join(REPO, "include")]
+    libdirs = ce.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=_c_ops_ext",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", "-DUSE_ROCM=1", "-D__HIP_PLATFORM_AMD__=1",
+           *[f"-I{i}" for i in incs], os.path.join(CSRC, EXT_SRC), "-o", out + ".tmp",
+           *[f"-L{d}" for d in libdirs], *[f"-Wl,-rpath,{d}" for d in libdirs],
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch binding build failed:\n{res.stderr[-4000:]}")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def build(jobs: int = 4, verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
@@ -70,6 +102,7 @@ def build(jobs: int = 4, verbose: bool = False) -> str:
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}")
+    build_torch_binding(verbose)
     return OUT
 
 

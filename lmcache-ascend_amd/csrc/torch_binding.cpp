@@ -1,0 +1,187 @@
+// Thin pybind11 binding of the per-call hot entry points for torch callers.
+//
+// The reference's callers issue one gather/scatter call per chunk or per
+// layer (lmcache_ascend/v1/npu_connector/npu_connectors.py:1146-1158,
+// 608-616), so host cost per call matters.  This module reads at::Tensor
+// geometry and the current HIP stream in C++ and calls the C ABI of
+// liblmcache_amd.so directly; argument meaning, defaults and exception types
+// are those of the reference's pybind module (csrc/pybind.cpp:364-481).
+//
+// The module does not link liblmcache_amd.so: `bind()` receives the
+// addresses of the C ABI functions from the library instance the Python
+// package already loaded, so both call paths share one library.
+#include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/lmcache_amd.h"
+
+namespace py = pybind11;
+
+namespace {
+
+using MultiFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, int32_t, int64_t,
+                        int32_t, int32_t, int32_t, int64_t, int64_t, int64_t, void *);
+using SingleFn = int (*)(const lmc_tensor *, const lmc_tensor *, int32_t, const lmc_tensor *, int32_t,
+                         int32_t, int32_t, int32_t, int64_t, int64_t, int64_t, void *);
+using FlashFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, const lmc_tensor *,
+                        int32_t, void *);
+using RopeFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, int64_t,
+                       const lmc_tensor *, int32_t, void *);
+using ErrFn = const char *(*)();
+
+struct Table {
+  MultiFn multi = nullptr;
+  SingleFn single = nullptr;
+  FlashFn load_flash = nullptr;
+  FlashFn reshape_flash = nullptr;
+  RopeFn rope = nullptr;
+  ErrFn last_error = nullptr;
+} g;
+
+int32_t dtype_code(at::ScalarType t) {
+  switch (t) {
+  case at::kByte: return LMC_U8;
+  case at::kChar: return LMC_I8;
+  case at::kShort: return LMC_I16;
+  case at::kInt: return LMC_I32;
+  case at::kLong: return LMC_I64;
+  case at::kHalf: return LMC_F16;
+  case at::kBFloat16: return LMC_BF16;
+  case at::kFloat: return LMC_F32;
+  default: throw std::runtime_error("ScalarType not supported.");
+  }
+}
+
+lmc_tensor desc(const at::Tensor &t) {
+  lmc_tensor d{};
+  const int64_t n = t.dim();
+  if (n > LMC_MAX_DIMS) throw std::runtime_error("tensors of more than 6 dims are not supported");
+  d.data = t.data_ptr();
+  d.dtype = dtype_code(t.scalar_type());
+  if (t.is_cuda()) d.device = t.get_device();
+  else if (t.is_cpu()) d.device = -1;
+  else throw std::runtime_error("Invalid device. Device must be a GPU or pinned cpu.");
+  d.ndim = static_cast<int32_t>(n);
+  const auto sz = t.sizes();
+  const auto st = t.strides();
+  for (int64_t i = 0; i < n; ++i) {
+    d.sizes[i] = sz[i];
+    d.strides[i] = st[i];
+  }
+  return d;
+}
+
+void check_bound() {
+  if (g.last_error == nullptr) throw std::runtime_error("lmcache_amd binding used before bind()");
+}
+
+void raise_for(int status) {
+  if (status == LMC_OK) return;
+  const std::string msg = g.last_error ? g.last_error() : "";
+  if (status == LMC_ERR_VALUE) throw py::value_error(msg);
+  if (status == LMC_ERR_NOT_IMPLEMENTED) {
+    PyErr_SetString(PyExc_NotImplementedError, msg.c_str());
+    throw py::error_already_set();
+  }
+  throw std::runtime_error(msg);
+}
+
+void *stream_of(int device) { return c10::hip::getCurrentHIPStream(device).stream(); }
+
+int device_of(const at::Device &d, const at::Tensor &fallback) {
+  if (d.is_cuda()) return d.has_index() ? d.index() : c10::hip::current_device();
+  if (fallback.is_cuda()) return fallback.get_device();
+  return c10::hip::current_device();
+}
+
+void multi_layer_kv_transfer(at::Tensor &key_value, const at::Tensor &key_value_ptrs,
+                             const at::Tensor &slot_mapping, const at::Device &paged_memory_device,
+                             int64_t page_buffer_size, bool direction, bool use_mla,
+                             int64_t kvcache_format_raw, int64_t k_hidden_dims,
+                             int64_t v_hidden_dims, int64_t dsa_hidden_dims) {
+  check_bound();
+  const int dev = device_of(paged_memory_device, key_value_ptrs);
+  const lmc_tensor a = desc(key_value), p = desc(key_value_ptrs), s = desc(slot_mapping);
+  raise_for(g.multi(&a, &p, &s, dev, page_buffer_size, direction, use_mla,
+                    static_cast<int32_t>(kvcache_format_raw), k_hidden_dims, v_hidden_dims,
+                    dsa_hidden_dims, stream_of(dev)));
+}
+
+std::vector<at::Tensor> normalize_kv_caches(const py::object &obj) {
+  // csrc/pybind.cpp:22-31: a Tensor or a tuple of Tensors.
+  if (THPVariable_Check(obj.ptr())) return {obj.cast<at::Tensor>()};
+  if (py::isinstance<py::tuple>(obj)) return obj.cast<std::vector<at::Tensor>>();
+  throw std::runtime_error("vllm_kv_caches must be a Tensor or a tuple of Tensors");
+}
+
+void single_layer_kv_transfer(at::Tensor &lmc, const py::object &caches_obj,
+                              const at::Tensor &slot_mapping, bool direction,
+                              int64_t kvcache_format_raw, bool token_major, bool vllm_two_major,
+                              int64_t k_hidden_dims, int64_t v_hidden_dims,
+                              int64_t dsa_hidden_dims) {
+  check_bound();
+  const std::vector<at::Tensor> caches = normalize_kv_caches(caches_obj);
+  std::vector<lmc_tensor> cd;
+  cd.reserve(caches.size());
+  int dev = -1;
+  for (const auto &c : caches) {
+    cd.push_back(desc(c));
+    if (dev < 0 && c.is_cuda()) dev = c.get_device();
+  }
+  if (dev < 0) dev = slot_mapping.is_cuda() ? slot_mapping.get_device() : c10::hip::current_device();
+  const lmc_tensor a = desc(lmc), s = desc(slot_mapping);
+  raise_for(g.single(&a, cd.data(), static_cast<int32_t>(cd.size()), &s, direction,
+                     static_cast<int32_t>(kvcache_format_raw), token_major, vllm_two_major,
+                     k_hidden_dims, v_hidden_dims, dsa_hidden_dims, stream_of(dev)));
+}
+
+void flash(FlashFn fn, at::Tensor &kv, at::Tensor &kc, at::Tensor &vc, at::Tensor &slots,
+           int64_t layer_idx) {
+  check_bound();
+  const int dev = kc.is_cuda() ? kc.get_device() : c10::hip::current_device();
+  const lmc_tensor a = desc(kv), k = desc(kc), v = desc(vc), s = desc(slots);
+  raise_for(fn(&a, &k, &v, &s, static_cast<int32_t>(layer_idx), stream_of(dev)));
+}
+
+void rotary_embedding_k_fused(const at::Tensor &old_pos, const at::Tensor &new_pos, at::Tensor &key,
+                              int64_t head_size, const at::Tensor &cos_sin_cache, bool is_neox) {
+  check_bound();
+  const int dev = key.is_cuda() ? key.get_device() : c10::hip::current_device();
+  const lmc_tensor a = desc(old_pos), b = desc(new_pos), k = desc(key), c = desc(cos_sin_cache);
+  raise_for(g.rope(&a, &b, &k, head_size, &c, is_neox, stream_of(dev)));
+}
+
+void bind(uintptr_t multi, uintptr_t single, uintptr_t load_flash, uintptr_t reshape_flash,
+          uintptr_t rope, uintptr_t last_error) {
+  g.multi = reinterpret_cast<MultiFn>(multi);
+  g.single = reinterpret_cast<SingleFn>(single);
+  g.load_flash = reinterpret_cast<FlashFn>(load_flash);
+  g.reshape_flash = reinterpret_cast<FlashFn>(reshape_flash);
+  g.rope = reinterpret_cast<RopeFn>(rope);
+  g.last_error = reinterpret_cast<ErrFn>(last_error);
+}
+
+} // namespace
+
+PYBIND11_MODULE(_c_ops_ext, m) {
+  m.def("bind", &bind);
+  m.def("multi_layer_kv_transfer", &multi_layer_kv_transfer);
+  m.def("single_layer_kv_transfer", &single_layer_kv_transfer, py::arg("lmc_key_value_cache"),
+        py::arg("vllm_kv_caches"), py::arg("slot_mapping"), py::arg("direction"),
+        py::arg("kvcache_format_raw"), py::arg("token_major") = false,
+        py::arg("vllm_two_major") = false, py::arg("k_hidden_dims") = 0,
+        py::arg("v_hidden_dims") = 0, py::arg("dsa_hidden_dims") = 0);
+  m.def("load_and_reshape_flash",
+        [](at::Tensor &kv, at::Tensor &kc, at::Tensor &vc, at::Tensor &s, int64_t layer) {
+          flash(g.load_flash, kv, kc, vc, s, layer);
+        });
+  m.def("reshape_and_cache_back_flash",
+        [](at::Tensor &kv, at::Tensor &kc, at::Tensor &vc, at::Tensor &s, int64_t layer) {
+          flash(g.reshape_flash, kv, kc, vc, s, layer);
+        });
+  m.def("rotary_embedding_k_fused", &rotary_embedding_k_fused);
+}

@@ -25,6 +25,29 @@ from . import _lib
 
 _L = _lib.load()
 
+
+def _addr(name: str) -> int:
+    return ctypes.cast(getattr(_L, name), ctypes.c_void_p).value
+
+
+# The C++ binding (csrc/torch_binding.cpp) reads tensor geometry and the HIP
+# stream in C++ for the per-call entry points; it calls the functions of the
+# library loaded above.  Without it the same functions are called through
+# ctypes.
+try:
+    from . import _c_ops_ext as _ext
+
+    _ext.bind(
+        _addr("lmc_multi_layer_kv_transfer"),
+        _addr("lmc_single_layer_kv_transfer"),
+        _addr("lmc_load_and_reshape_flash"),
+        _addr("lmc_reshape_and_cache_back_flash"),
+        _addr("lmc_rotary_embedding_k_fused"),
+        _addr("lmc_last_error"),
+    )
+except ImportError:
+    _ext = None
+
 _DTYPES = {
     torch.uint8: _lib.U8,
     torch.int8: _lib.I8,
@@ -117,6 +140,23 @@ def multi_layer_kv_transfer(
     dsa_hidden_dims: int = 0,
 ) -> None:
     """csrc/mem_kernels.cpp:75-111.  direction=True: paged -> key_value."""
+    if _ext is not None:
+        _ext.multi_layer_kv_transfer(
+            key_value, key_value_ptrs, slot_mapping, torch.device(paged_memory_device),
+            int(page_buffer_size), bool(direction), bool(use_mla), int(kvcache_format_raw),
+            int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims),
+        )
+        return
+    _multi_layer_kv_transfer_ctypes(
+        key_value, key_value_ptrs, slot_mapping, paged_memory_device, page_buffer_size, direction,
+        use_mla, kvcache_format_raw, k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
+    )
+
+
+def _multi_layer_kv_transfer_ctypes(
+    key_value, key_value_ptrs, slot_mapping, paged_memory_device, page_buffer_size, direction,
+    use_mla, kvcache_format_raw, k_hidden_dims=0, v_hidden_dims=0, dsa_hidden_dims=0,
+) -> None:
     dev = _device_index(paged_memory_device, key_value_ptrs)
     a, p, s = _desc(key_value), _desc(key_value_ptrs), _desc(slot_mapping)
     _run(
@@ -222,6 +262,23 @@ def single_layer_kv_transfer(
     dsa_hidden_dims: int = 0,
 ) -> None:
     """csrc/mem_kernels.cpp:265-334 (pybind keywords csrc/pybind.cpp:367-372)."""
+    if _ext is not None:
+        _ext.single_layer_kv_transfer(
+            lmc_key_value_cache, vllm_kv_caches, slot_mapping, bool(direction), int(kvcache_format_raw),
+            bool(token_major), bool(vllm_two_major), int(k_hidden_dims), int(v_hidden_dims),
+            int(dsa_hidden_dims),
+        )
+        return
+    _single_layer_kv_transfer_ctypes(
+        lmc_key_value_cache, vllm_kv_caches, slot_mapping, direction, kvcache_format_raw, token_major,
+        vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
+    )
+
+
+def _single_layer_kv_transfer_ctypes(
+    lmc_key_value_cache, vllm_kv_caches, slot_mapping, direction, kvcache_format_raw, token_major=False,
+    vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0, dsa_hidden_dims=0,
+) -> None:
     caches = _normalize_kv_caches(vllm_kv_caches)
     n = len(caches)
     arr = (_lib.LmcTensor * max(n, 1))()
@@ -240,6 +297,9 @@ def single_layer_kv_transfer(
 
 def load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, layer_idx) -> None:
     """csrc/mem_kernels.cpp:1341-1387: key_value[:, layer_idx] <- paged rows."""
+    if _ext is not None:
+        _ext.load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, int(layer_idx))
+        return
     dev = _device_index(key_cache)
     a, k, v, s = _desc(key_value), _desc(key_cache), _desc(value_cache), _desc(slot_mapping)
     _run(_L.lmc_load_and_reshape_flash(_ref(a), _ref(k), _ref(v), _ref(s), int(layer_idx), _stream(dev)))
@@ -247,6 +307,9 @@ def load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, laye
 
 def reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping, layer_idx) -> None:
     """csrc/mem_kernels.cpp:1389-1440: paged rows <- key_value[:, layer_idx]."""
+    if _ext is not None:
+        _ext.reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping, int(layer_idx))
+        return
     dev = _device_index(key_cache)
     a, k, v, s = _desc(key_value), _desc(key_cache), _desc(value_cache), _desc(slot_mapping)
     _run(
@@ -298,6 +361,9 @@ def decode_fast_prefsum(cdf, bytestreams, lengths, output) -> None:
 
 def rotary_embedding_k_fused(oldPositions, newPositions, key, headSize, cosSinCache, isNeox) -> None:
     """csrc/pos_kernels.cpp:158-196: key rotated in place, old -> new."""
+    if _ext is not None:
+        _ext.rotary_embedding_k_fused(oldPositions, newPositions, key, int(headSize), cosSinCache, bool(isNeox))
+        return
     dev = _device_index(key)
     a, b, k, c = _desc(oldPositions), _desc(newPositions), _desc(key), _desc(cosSinCache)
     _run(

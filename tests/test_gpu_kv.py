@@ -540,3 +540,30 @@ def test_llama8b_shape_full_size_round_trip(ops):
         assert torch.equal(t.reshape(-1, W)[slots].view(torch.int16), s.view(torch.int16))
     checksum_after = [t.view(torch.int16).to(torch.int64).sum().item() for t in flat[:4]]
     assert checksum_before == checksum_after
+
+
+def test_binding_and_ctypes_paths_agree(ops):
+    """The C++ binding and the ctypes calls reach the same library functions
+    and move the same bytes."""
+    gen = torch.Generator().manual_seed(808)
+    L, NB, BS, H, D, T = 4, 64, 16, 8, 128, 300
+    W = H * D
+    pbs = NB * BS
+    layers = _paged(2, L, NB, BS, H, D, gen)
+    flat = _flat_tensors(layers)
+    ptrs = ptr_table(flat, DEV)
+    slots = torch.tensor(sample_slots(pbs, T, seed=8), device=DEV)
+    a = torch.zeros((2, L, T, W), dtype=torch.bfloat16, device=DEV)
+    b = torch.zeros_like(a)
+    assert ops._ext is not None, "the C++ binding was not built"
+    ops.multi_layer_kv_transfer(a, ptrs, slots, torch.device(DEV), pbs, True, False, 2, W, W, 0)
+    ops._multi_layer_kv_transfer_ctypes(b, ptrs, slots, torch.device(DEV), pbs, True, False, 2, W, W, 0)
+    _sync()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    c = torch.zeros((2, T, W), dtype=torch.bfloat16, device=DEV)
+    d = torch.zeros_like(c)
+    ops.single_layer_kv_transfer(c, layers[1], slots, True, 2)
+    ops._single_layer_kv_transfer_ctypes(d, layers[1], slots, True, 2)
+    _sync()
+    assert torch.equal(c.view(torch.int16), d.view(torch.int16))
+    assert torch.equal(c.view(torch.int16), a[:, 1].view(torch.int16))
