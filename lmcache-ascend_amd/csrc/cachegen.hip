@@ -38,11 +38,35 @@ constexpr int kLanes = 256;
 constexpr int kMaxBins = 64;
 constexpr int kPrec = 16;
 constexpr int kMaxLen = 12;
+constexpr int kBatch = 32;  // symbol loads in flight per lane
 
-// Unpacks one stream's CDF row into LDS column `col` as
-// (base << 8) | length per symbol (rules L1-L3).  `cur` is the unwrapped
-// base of symbol s, `next` that of s + 1; once a base has wrapped to
-// 0x10000, every later one is 0x10000 as well.
+// Copies `count` (>= 1) consecutive int16 CDF entries into LDS with every
+// lane of the block, 8 loads per lane in flight: each load address is
+// clamped into [0, count) so the batch has no branches between its loads.
+template <int LANES>
+__device__ __forceinline__ void stage_rows(const int16_t *__restrict__ src,
+                                           int count, int16_t *dst) {
+  constexpr int kB = 8;
+  for (int i0 = 0; i0 < count; i0 += LANES * kB) {
+    int16_t v[kB];
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = i0 + k * LANES + static_cast<int>(threadIdx.x);
+      v[k] = src[i < count ? i : count - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = i0 + k * LANES + static_cast<int>(threadIdx.x);
+      if (i < count) dst[i] = v[k];
+    }
+  }
+}
+
+// Unpacks one stream's CDF row (staged in LDS) into the LDS column `col`
+// (stride LANES) as (base << 8) | length per symbol (rules L1-L3).  `cur`
+// is the unwrapped base of symbol s, `next` that of s + 1; once a base has
+// wrapped to 0x10000, every later one is 0x10000 as well.
+template <int LANES>
 __device__ __forceinline__ void unpack_row(const int16_t *row, int nb,
                                            uint32_t *col) {
   uint32_t cur_raw = static_cast<uint16_t>(row[0]);
@@ -59,7 +83,7 @@ __device__ __forceinline__ void unpack_row(const int16_t *row, int nb,
       const uint32_t w = next - cur;
       if (w != 0) len = kPrec - (31 - __builtin_clz(w));
     }
-    col[s * kLanes] = (cur << 8) | static_cast<uint32_t>(len);
+    col[s * LANES] = (cur << 8) | static_cast<uint32_t>(len);
     cur = next;
     cur_raw = next_raw;
   }
@@ -75,10 +99,17 @@ __global__ void __launch_bounds__(kLanes)
   uint32_t *col = lds + threadIdx.x;
   for (int s = 0; s < nb; ++s) col[s * kLanes] = 0;
   const uint8_t *p = in + static_cast<int64_t>(l) * T * C + c;
-#pragma unroll 8
-  for (int t = 0; t < T; ++t) {
-    const uint32_t s = p[static_cast<int64_t>(t) * C];
-    if (s < static_cast<uint32_t>(nb)) col[s * kLanes] += 1u;
+  // kBatch symbol loads in flight per lane, then no-return LDS adds (each
+  // lane owns its histogram column, so there is no contention and no
+  // read-modify-write latency chain).
+  for (int t0 = 0; t0 < T; t0 += kBatch) {
+    uint32_t sym[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      sym[i] = t0 + i < T ? p[static_cast<int64_t>(t0 + i) * C] : 0xFFu;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (sym[i] < static_cast<uint32_t>(nb)) atomicAdd(&col[sym[i] * kLanes], 1u);
   }
   // Code lengths (rule L4); entries become (count << 5) | length.
   uint32_t n = 0;
@@ -148,48 +179,67 @@ __device__ __forceinline__ void put_bytes(uint8_t *row, int64_t chunk,
     if (at + b < chunk) row[at + b] = static_cast<uint8_t>(word >> (24 - 8 * b));
 }
 
-__global__ void __launch_bounds__(kLanes)
+// Encode: 64 streams per block (one wave); the block's 64 CDF rows are
+// contiguous in memory and staged through LDS with coalesced loads.
+constexpr int kEncLanes = 64;
+
+__global__ void __launch_bounds__(kEncLanes)
     encode_kernel(const int16_t *__restrict__ cdf,
                   const uint8_t *__restrict__ in, int T, int C, int nb,
                   uint8_t *__restrict__ out, int64_t chunk,
                   int32_t *__restrict__ lens, int tiles, int word_stores) {
   extern __shared__ uint32_t lds[];
-  const int l = blockIdx.x / tiles;
-  const int c = (blockIdx.x % tiles) * kLanes + threadIdx.x;
-  if (c >= C) return;
-  const int64_t stream = static_cast<int64_t>(l) * C + c;
+  // [nb][kEncLanes] u32 code table, then [kEncLanes][nb + 1] int16 rows.
   uint32_t *col = lds + threadIdx.x;
-  unpack_row(cdf + stream * (nb + 1), nb, col);
+  int16_t *stage = reinterpret_cast<int16_t *>(lds + nb * kEncLanes);
+  const int l = blockIdx.x / tiles;
+  const int c0 = (blockIdx.x % tiles) * kEncLanes;
+  const int cnt = C - c0 < kEncLanes ? C - c0 : kEncLanes;
+  const int64_t s0 = static_cast<int64_t>(l) * C + c0;
+  stage_rows<kEncLanes>(cdf + s0 * (nb + 1), cnt * (nb + 1), stage);
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) >= cnt) return;
+  const int c = c0 + static_cast<int>(threadIdx.x);
+  const int64_t stream = s0 + threadIdx.x;
+  unpack_row<kEncLanes>(stage + threadIdx.x * (nb + 1), nb, col);
   // Code table: (code << 5) | length.
   for (int s = 0; s < nb; ++s) {
-    const uint32_t e = col[s * kLanes];
+    const uint32_t e = col[s * kEncLanes];
     const uint32_t len = e & 0xFFu;
     const uint32_t base = e >> 8;
     const uint32_t code =
         len ? (base >> (kPrec - len)) & ((1u << len) - 1u) : 0u;
-    col[s * kLanes] = (code << 5) | len;
+    col[s * kEncLanes] = (code << 5) | len;
   }
   uint8_t *row = out + stream * chunk;
   const uint8_t *p = in + static_cast<int64_t>(l) * T * C + c;
   uint64_t acc = 0;
   int nbits = 0;
   int64_t wpos = 0;  // bytes already written
-#pragma unroll 4
-  for (int t = 0; t < T; ++t) {
-    const uint32_t s = p[static_cast<int64_t>(t) * C];
-    if (s >= static_cast<uint32_t>(nb)) continue;
-    const uint32_t e = col[s * kLanes];
-    const int len = static_cast<int>(e & 31u);
-    acc = (acc << len) | (e >> 5);
-    nbits += len;
-    if (nbits >= 32) {
-      const uint32_t word = static_cast<uint32_t>(acc >> (nbits - 32));
-      if (word_stores && wpos + 4 <= chunk)
-        *reinterpret_cast<uint32_t *>(row + wpos) = __builtin_bswap32(word);
-      else
-        put_bytes(row, chunk, wpos, word, 4);
-      wpos += 4;
-      nbits -= 32;
+  for (int t0 = 0; t0 < T; t0 += kBatch) {
+    // All symbol loads of the batch in flight, then all table lookups, then
+    // the serial bit packing.
+    uint32_t e[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      e[i] = t0 + i < T ? p[static_cast<int64_t>(t0 + i) * C] : 0xFFu;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      e[i] = e[i] < static_cast<uint32_t>(nb) ? col[e[i] * kEncLanes] : 0u;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int len = static_cast<int>(e[i] & 31u);
+      acc = (acc << len) | (e[i] >> 5);
+      nbits += len;
+      if (nbits >= 32) {
+        const uint32_t word = static_cast<uint32_t>(acc >> (nbits - 32));
+        if (word_stores && wpos + 4 <= chunk)
+          *reinterpret_cast<uint32_t *>(row + wpos) = __builtin_bswap32(word);
+        else
+          put_bytes(row, chunk, wpos, word, 4);
+        wpos += 4;
+        nbits -= 32;
+      }
     }
   }
   if (nbits > 0) {
@@ -199,43 +249,353 @@ __global__ void __launch_bounds__(kLanes)
   lens[stream] = static_cast<int32_t>(wpos + ((nbits + 7) >> 3));
 }
 
-__global__ void __launch_bounds__(kLanes)
+// Decode: 64 streams per block (one wave) and 40 KiB of LDS per block, so
+// the four blocks of a CU's four SIMDs fit its 160 KiB.  The block's 64
+// streams are adjacent in the byte buffer; their CDF rows and (up to the
+// window size) their bytes are staged into LDS with coalesced 16-byte
+// loads, so the per-symbol loop touches no global memory except for
+// streams that do not fit the window.
+//
+// Symbol lookup (rule L6) is table driven.  Bases are multiples of 16, so
+// the top 12 bits of the 16-bit window decide the symbol.  L1 has one
+// entry per 7-bit prefix: symbol | length << 8 when one symbol owns the
+// prefix's whole range; 0x8000 | k << 8 | s_first when symbol boundaries
+// fall inside it, k naming one of the stream's kSubTables L2 tables whose
+// 32 one-byte entries (next 5 bits) hold (s - s_first) << 4 | length; and
+// kOverflow when the stream ran out of L2 tables (or a prefix spans more
+// than 16 symbols), which falls back to a binary search over the bases.
+constexpr int kDecLanes = 64;
+constexpr int kDirectBits = 7;
+constexpr int kSubBits = 5;
+constexpr int kSubTables = 4;
+constexpr uint32_t kOverflow = 0xFFFFu;
+constexpr int kDecLds = 40 * 1024;
+constexpr int kL1Bytes = (1 << kDirectBits) * kDecLanes * 2;
+constexpr int kL2Bytes = kSubTables * (1 << kSubBits) * kDecLanes;
+constexpr int kObufBytes = 4 * kDecLanes;
+constexpr int kRowsOff = kL1Bytes + kL2Bytes + kObufBytes;
+constexpr int kStageBatch = 8;  // 16-byte loads in flight per lane
+
+// Copies n16 16-byte chunks starting at the 16-byte aligned global address
+// `src` into LDS with every lane of the block, kStageBatch loads per lane
+// in flight.  Indexes past the end are clamped to the last chunk, whose
+// slot then receives the same bytes from several lanes.  kSwap stores each
+// dword byte-reversed (big-endian order of the stream bits).
+template <bool kSwap>
+__device__ __forceinline__ void stage16(uintptr_t src, int n16, uint8_t *dst) {
+  const uint4 *s = reinterpret_cast<const uint4 *>(src);
+  uint4 *d = reinterpret_cast<uint4 *>(dst);
+  for (int j0 = 0; j0 < n16; j0 += kDecLanes * kStageBatch) {
+    int idx[kStageBatch];
+    uint4 v[kStageBatch];
+#pragma unroll
+    for (int k = 0; k < kStageBatch; ++k) {
+      const int j = j0 + k * kDecLanes + static_cast<int>(threadIdx.x);
+      idx[k] = j < n16 ? j : n16 - 1;
+      v[k] = s[idx[k]];
+    }
+#pragma unroll
+    for (int k = 0; k < kStageBatch; ++k) {
+      uint4 w = v[k];
+      if (kSwap) {
+        w.x = __builtin_bswap32(w.x);
+        w.y = __builtin_bswap32(w.y);
+        w.z = __builtin_bswap32(w.z);
+        w.w = __builtin_bswap32(w.w);
+      }
+      d[idx[k]] = w;
+    }
+  }
+}
+
+// Bases and lengths (rules L1-L3) read straight from a staged raw CDF row.
+// `wrap` is the first symbol whose entry is below its predecessor's (nb if
+// none): it and every later symbol have base 0x10000.
+struct StagedRow {
+  const int16_t *r;
+  int wrap;
+  __device__ __forceinline__ uint32_t base(int s) const {
+    return s >= wrap ? 0x10000u : (static_cast<uint32_t>(static_cast<uint16_t>(r[s])) & 0xFFF0u);
+  }
+  __device__ __forceinline__ int len(int s) const {
+    const int nib = static_cast<uint16_t>(r[s]) & 0xF;
+    if (nib) return nib;
+    const uint32_t w = base(s + 1) - base(s);
+    return w ? kPrec - (31 - __builtin_clz(w)) : 0;
+  }
+};
+
+// Per-lane decode tables: L1 and L2 columns of stride kDecLanes.
+struct DecTables {
+  uint16_t *l1;
+  uint8_t *l2;
+  StagedRow row;
+  int nb;
+  int top;  // largest power of two below nb (1 if nb <= 2)
+
+  // Builds L1/L2 from the staged row in one pass over the symbols (a loop
+  // every lane runs in step).  Symbol s owns the windows [lo, hi): lo is
+  // its base (0 for s = 0, which also takes windows below the first base),
+  // hi the next base.  Prefixes entirely inside [lo, hi) get a direct
+  // entry; a prefix holding a boundary is opened by the symbol covering its
+  // start and filled by that symbol and the following ones.  Also finds
+  // row.wrap.
+  __device__ __forceinline__ void build() {
+    constexpr uint32_t span = 1u << (kPrec - kDirectBits);
+    constexpr uint32_t sub = 1u << (kPrec - kDirectBits - kSubBits);
+    row.wrap = nb;
+    uint32_t raw = static_cast<uint16_t>(row.r[0]);
+    uint32_t base = raw & 0xFFF0u;
+    uint32_t last = base;  // last base before any wrap
+    int open_k = -1, open_first = 0, nsub = 0;
+    for (int s = 0; s < nb; ++s) {
+      uint32_t next = 0x10000u, next_raw = 0;
+      if (s + 1 < nb) {
+        next_raw = static_cast<uint16_t>(row.r[s + 1]);
+        const uint32_t nbase = next_raw & 0xFFF0u;
+        if (row.wrap == nb && nbase >= last) {
+          next = nbase;
+          last = nbase;
+        } else if (row.wrap == nb) {
+          row.wrap = s + 1;
+        }
+      }
+      int len = static_cast<int>(raw & 0xFu);
+      if (len == 0) {
+        const uint32_t w = next - base;
+        if (w != 0) len = kPrec - (31 - __builtin_clz(w));
+      }
+      const uint32_t lo = s == 0 ? 0u : base, hi = next;
+      if (hi > lo) {
+        const uint32_t ent = static_cast<uint32_t>(s) | (static_cast<uint32_t>(len) << 8);
+        uint32_t e = lo / span;
+        if (lo % span) {  // inside a prefix opened by an earlier symbol
+          if (open_k >= 0) {
+            const int ds = s - open_first;
+            if (ds > 15) {
+              l1[e * kDecLanes] = static_cast<uint16_t>(kOverflow);
+              open_k = -1;
+            } else {
+              const uint32_t j1 = hi - e * span < span ? (hi - e * span) / sub : span / sub;
+              for (uint32_t j = (lo % span) / sub; j < j1; ++j)
+                l2[(open_k * (1 << kSubBits) + j) * kDecLanes] =
+                    static_cast<uint8_t>((ds << 4) | len);
+            }
+          }
+          ++e;
+        }
+        for (; e < hi / span; ++e) l1[e * kDecLanes] = static_cast<uint16_t>(ent);
+        if ((hi % span) && lo <= hi - hi % span) {  // opens the prefix holding hi
+          e = hi / span;
+          if (nsub < kSubTables) {
+            open_k = nsub++;
+            open_first = s;
+            l1[e * kDecLanes] = static_cast<uint16_t>(0x8000u | (open_k << 8) | s);
+            for (uint32_t j = 0; j < (hi % span) / sub; ++j)
+              l2[(open_k * (1 << kSubBits) + j) * kDecLanes] = static_cast<uint8_t>(len);
+          } else {
+            open_k = -1;
+            l1[e * kDecLanes] = static_cast<uint16_t>(kOverflow);
+          }
+        }
+      }
+      raw = next_raw;
+      base = next;
+    }
+    top = 1;
+    while (top * 2 < nb) top *= 2;
+  }
+
+  // Symbol and code length for the 16-bit window v.
+  __device__ __forceinline__ void lookup(uint32_t v, int &s, int &len) const {
+    const uint32_t d = l1[(v >> (kPrec - kDirectBits)) * kDecLanes];
+    if (d < 0x8000u) {
+      s = static_cast<int>(d & 0xFFu);
+      len = static_cast<int>(d >> 8);
+    } else if (d != kOverflow) {
+      const uint32_t j = (v >> (kPrec - kDirectBits - kSubBits)) & ((1u << kSubBits) - 1);
+      const uint32_t x = l2[(((d >> 8) & 0x7Fu) * (1 << kSubBits) + j) * kDecLanes];
+      s = static_cast<int>((d & 0xFFu) + (x >> 4));
+      len = static_cast<int>(x & 0xFu);
+    } else {
+      s = 0;
+      for (int step = top; step > 0; step >>= 1)
+        if (s + step < nb && row.base(s + step) <= v) s += step;
+      len = row.len(s);
+    }
+  }
+};
+
+// Bytes of the aligned dword at address `a` that lie in [lo, hi), as a mask
+// over the dword's little-endian value.
+__device__ __forceinline__ uint32_t live_mask(uintptr_t a, uintptr_t lo, uintptr_t hi) {
+  const int64_t from = static_cast<int64_t>(lo) - static_cast<int64_t>(a);
+  const int64_t to = static_cast<int64_t>(hi) - static_cast<int64_t>(a);
+  const int f = from < 0 ? 0 : (from > 4 ? 4 : static_cast<int>(from));
+  const int t = to < 0 ? 0 : (to > 4 ? 4 : static_cast<int>(to));
+  const uint32_t below_t = t >= 4 ? ~0u : ((1u << (8 * t)) - 1u);
+  const uint32_t below_f = f >= 4 ? ~0u : ((1u << (8 * f)) - 1u);
+  return below_t & ~below_f;
+}
+
+// Big-endian dword of the staged window at byte offset q (a multiple of 4),
+// with the bytes at or past `hi` (an offset too) zeroed.  The read is
+// clamped to the window's last dword; whatever it returns past hi is
+// masked off.
+__device__ __forceinline__ uint32_t win_word(const uint32_t *win, uint32_t last, uint32_t q,
+                                             uint32_t hi) {
+  const uint32_t w = win[(q < last ? q : last) >> 2];
+  const int t = static_cast<int>(hi) - static_cast<int>(q);
+  const int k = t < 0 ? 0 : (t > 4 ? 4 : t);
+  return k >= 4 ? w : (w & ~(~0u >> (8 * k)));
+}
+
+// All 64 streams of the block lie in the window: L1/L2 lookups, window
+// dwords prefetched one refill ahead, and symbols transposed through LDS so
+// each lane stores one dword (4 channels of one token) per 4 tokens.
+__device__ __forceinline__ void decode_block_fast(const DecTables &tb, int T, int C,
+                                                  const uint32_t *win, uint32_t win_last,
+                                                  uint32_t lo, uint32_t hi, uint8_t *obuf,
+                                                  uint8_t *__restrict__ out_blk) {
+  const int lane = static_cast<int>(threadIdx.x);
+  uint32_t q = lo & ~3u;
+  uint64_t buf = static_cast<uint64_t>(win_word(win, win_last, q, hi)) << 32;
+  q += 4;
+  buf <<= 8 * (lo & 3u);
+  int have = 32 - 8 * static_cast<int>(lo & 3u);
+  uint32_t nxt = win_word(win, win_last, q, hi);
+  q += 4;
+  // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
+  uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
+  const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
+  for (int t = 0; t < T; ++t) {
+    if (have <= 32) {  // leaves more than 32 bits; codes are <= 15
+      buf |= static_cast<uint64_t>(nxt) << (32 - have);
+      have += 32;
+      nxt = win_word(win, win_last, q, hi);
+      q += 4;
+    }
+    int s, len;
+    tb.lookup(static_cast<uint32_t>(buf >> 48), s, len);
+    obuf[(t & 3) * kDecLanes + lane] = static_cast<uint8_t>(s);
+    buf <<= len;
+    have -= len;
+    if ((t & 3) == 3) {
+      __syncthreads();
+      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      odst += step4;
+      __syncthreads();
+    }
+  }
+  if (T & 3) {
+    __syncthreads();
+    if ((lane >> 4) < (T & 3)) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+  }
+}
+
+// One stream occupying [lo, hi) (addresses), symbols to o[0], o[C], ...
+// kWin: every dword the stream needs is in the LDS window holding the bytes
+// from a_lo to a_hi, read with the index clamped into the window.
+// Otherwise dwords come from global memory, and only those holding a byte
+// of [lo, hi) are read.
+template <bool kWin>
+__device__ __forceinline__ void decode_stream(const DecTables &tb, int T, int C,
+                                              const uint8_t *__restrict__ bytes, const uint32_t *win,
+                                              uintptr_t a_lo, uintptr_t a_hi, uintptr_t lo,
+                                              uintptr_t hi, uint8_t *__restrict__ o) {
+  const uintptr_t base0 = reinterpret_cast<uintptr_t>(bytes);
+  auto word_at = [&](uintptr_t q) -> uint32_t {
+    if (kWin) {
+      const uint32_t last = static_cast<uint32_t>(a_hi - a_lo) - 4;
+      return win_word(win, last, static_cast<uint32_t>(q - a_lo), static_cast<uint32_t>(hi - a_lo));
+    }
+    uint32_t raw = 0;
+    if (q < hi) raw = *reinterpret_cast<const uint32_t *>(bytes + (q - base0));
+    return __builtin_bswap32(raw & live_mask(q, lo, hi));
+  };
+  uintptr_t q = lo & ~uintptr_t(3);
+  uint64_t buf = static_cast<uint64_t>(word_at(q)) << 32;
+  q += 4;
+  buf <<= 8 * (lo & 3);
+  int have = 32 - 8 * static_cast<int>(lo & 3);
+  for (int t = 0; t < T; ++t) {
+    if (have <= 32) {
+      buf |= static_cast<uint64_t>(word_at(q)) << (32 - have);
+      have += 32;
+      q += 4;
+    }
+    int s, len;
+    tb.lookup(static_cast<uint32_t>(buf >> 48), s, len);
+    o[static_cast<int64_t>(t) * C] = static_cast<uint8_t>(s);
+    buf <<= len;
+    have -= len;
+  }
+}
+
+__global__ void __launch_bounds__(kDecLanes)
     decode_kernel(const int16_t *__restrict__ cdf,
                   const uint8_t *__restrict__ bytes, int64_t nbytes,
                   const int32_t *__restrict__ prefix, int T, int C, int nb,
                   uint8_t *__restrict__ out, int tiles) {
-  extern __shared__ uint32_t lds[];
+  // [L1 u16][L2 u8][obuf: 4 tokens x 64 lanes][staged rows][byte window]
+  extern __shared__ uint32_t lds_words[];
+  uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
+  const int rows_cap = ((nb + 1) * kDecLanes * 2 + 32 + 15) & ~15;
+  const int win_off = kRowsOff + rows_cap;
+  const int win_cap = (kDecLds - win_off) & ~15;
   const int l = blockIdx.x / tiles;
-  const int c = (blockIdx.x % tiles) * kLanes + threadIdx.x;
-  if (c >= C) return;
-  const int64_t stream = static_cast<int64_t>(l) * C + c;
-  uint32_t *col = lds + threadIdx.x;
-  unpack_row(cdf + stream * (nb + 1), nb, col);
-  int64_t start = stream == 0 ? 0 : prefix[stream - 1];
-  int64_t end = prefix[stream];
-  start = start < 0 ? 0 : (start > nbytes ? nbytes : start);
-  end = end > nbytes ? nbytes : (end < start ? start : end);
-  uint64_t buf = 0;  // valid bits left-aligned
-  int have = 0;
-  int64_t rd = start;
-  uint8_t *o = out + static_cast<int64_t>(l) * T * C + c;
-  int top = 1;
-  while (top * 2 < nb) top *= 2;
-  for (int t = 0; t < T; ++t) {
-    while (have <= 56) {
-      const uint64_t b = rd < end ? bytes[rd] : 0u;
-      ++rd;
-      buf |= b << (56 - have);
-      have += 8;
-    }
-    const uint32_t v = static_cast<uint32_t>(buf >> 48);
-    int s = 0;
-    for (int step = top; step > 0; step >>= 1)
-      if (s + step < nb && (col[(s + step) * kLanes] >> 8) <= v) s += step;
-    const int len = static_cast<int>(col[s * kLanes] & 0xFFu);
-    o[static_cast<int64_t>(t) * C] = static_cast<uint8_t>(s);
-    buf <<= len;
-    have -= len;
+  const int c0 = (blockIdx.x % tiles) * kDecLanes;
+  const int cnt = C - c0 < kDecLanes ? C - c0 : kDecLanes;
+  const int64_t s0 = static_cast<int64_t>(l) * C + c0;
+  const int live = static_cast<int>(threadIdx.x) < cnt;
+  const int64_t stream = s0 + (live ? threadIdx.x : 0);
+  auto clampb = [&](int64_t x) { return x < 0 ? 0 : (x > nbytes ? nbytes : x); };
+  int64_t start = clampb(stream == 0 ? 0 : prefix[stream - 1]);
+  int64_t end = clampb(prefix[stream]);
+  end = end < start ? start : end;
+  const int64_t B0 = clampb(s0 == 0 ? 0 : prefix[s0 - 1]);
+  const int64_t B1 = clampb(prefix[s0 + cnt - 1]);
+  // Rows: bytes [R0, R1) from the 16-byte aligned address at or below R0.
+  const uintptr_t R0 = reinterpret_cast<uintptr_t>(cdf + s0 * (nb + 1));
+  const uintptr_t R1 = R0 + static_cast<uintptr_t>(cnt) * (nb + 1) * 2;
+  const uintptr_t r_lo = R0 & ~uintptr_t(15);
+  stage16<false>(r_lo, static_cast<int>((R1 - r_lo + 15) >> 4), lds + kRowsOff);
+  // Window: the block's bytes [B0, B1) from the 16-byte aligned address at
+  // or below B0, at most win_cap bytes.  Every chunk staged (rows or
+  // window) holds a byte of its range, so no load leaves the buffers' pages.
+  const uintptr_t base0 = reinterpret_cast<uintptr_t>(bytes);
+  const uintptr_t a_lo = (base0 + B0) & ~uintptr_t(15);
+  int n16 = 0;
+  if (B1 > B0) {
+    const uintptr_t want = base0 + B1 - a_lo;
+    const uintptr_t cap = static_cast<uintptr_t>(win_cap);
+    n16 = static_cast<int>(((want < cap ? want : cap) + 15) >> 4);
+  }
+  stage16<true>(a_lo, n16, lds + win_off);
+  __syncthreads();
+  const uintptr_t lo = base0 + static_cast<uintptr_t>(start);
+  const uintptr_t hi = base0 + static_cast<uintptr_t>(end);
+  const uintptr_t a_hi = a_lo + 16 * static_cast<uintptr_t>(n16);
+  const bool in_win = hi > lo && (lo & ~uintptr_t(3)) >= a_lo && ((hi + 3) & ~uintptr_t(3)) <= a_hi;
+  const bool fast = cnt == kDecLanes && (reinterpret_cast<uintptr_t>(out) & 3) == 0 && (C & 3) == 0 &&
+                    __all(in_win);
+  if (!live) return;
+  DecTables tb;
+  tb.l1 = reinterpret_cast<uint16_t *>(lds) + threadIdx.x;
+  tb.l2 = lds + kL1Bytes + threadIdx.x;
+  tb.row.r = reinterpret_cast<const int16_t *>(lds + kRowsOff + (R0 - r_lo)) + threadIdx.x * (nb + 1);
+  tb.nb = nb;
+  tb.build();
+  const uint32_t *win = reinterpret_cast<const uint32_t *>(lds + win_off);
+  uint8_t *out_blk = out + static_cast<int64_t>(l) * T * C + c0;
+  if (fast) {
+    decode_block_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
+                      static_cast<uint32_t>(lo - a_lo), static_cast<uint32_t>(hi - a_lo),
+                      lds + kL1Bytes + kL2Bytes, out_blk);
+  } else if (in_win) {
+    decode_stream<true>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + threadIdx.x);
+  } else {
+    decode_stream<false>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + threadIdx.x);
   }
 }
 
@@ -320,11 +680,12 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
     check(ob.sizes[0] == L && ob.sizes[1] == C, "output_buffer must be [L, C, chunk]");
     if (L == 0 || C == 0) return;
     DeviceGuard guard(in.device);
-    const int tiles = static_cast<int>((C + kLanes - 1) / kLanes);
-    const size_t lds = static_cast<size_t>(nb) * kLanes * 4;
+    const int tiles = static_cast<int>((C + kEncLanes - 1) / kEncLanes);
+    const size_t lds = static_cast<size_t>(nb) * kEncLanes * 4 +
+                       static_cast<size_t>(nb + 1) * kEncLanes * 2;
     const int word_stores =
         (chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(ob.data) & 3) == 0) ? 1 : 0;
-    hipLaunchKernelGGL(encode_kernel, dim3(L * tiles), dim3(kLanes), lds,
+    hipLaunchKernelGGL(encode_kernel, dim3(L * tiles), dim3(kEncLanes), lds,
                        static_cast<hipStream_t>(stream),
                        static_cast<const int16_t *>(cdf.data),
                        static_cast<const uint8_t *>(in.data), (int)T, (int)C,
@@ -376,9 +737,9 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf_t,
     check(numel(o) == L * T * C, "output must hold L * T * C symbols");
     if (L == 0 || C == 0 || T == 0) return;
     DeviceGuard guard(bs.device);
-    const int tiles = static_cast<int>((C + kLanes - 1) / kLanes);
-    const size_t lds = static_cast<size_t>(nb) * kLanes * 4;
-    hipLaunchKernelGGL(decode_kernel, dim3(L * tiles), dim3(kLanes), lds,
+    const int tiles = static_cast<int>((C + kDecLanes - 1) / kDecLanes);
+    const size_t lds = kDecLds;
+    hipLaunchKernelGGL(decode_kernel, dim3(L * tiles), dim3(kDecLanes), lds,
                        static_cast<hipStream_t>(stream),
                        static_cast<const int16_t *>(cdf.data),
                        static_cast<const uint8_t *>(bs.data), numel(bs),

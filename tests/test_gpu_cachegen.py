@@ -205,3 +205,43 @@ def test_decode_limits(ops):
                                 torch.zeros((1, 4, 32), dtype=torch.uint8, device=DEV))
     with pytest.raises(NotImplementedError):
         ops.decode_fast_new(None, None, None, None)
+
+
+def _arbitrary_cdf_rows(rng, L, C, nb):
+    """CDF rows a caller may build by hand: non-decreasing 16-bit bases in
+    steps of 16 with gaps and repeats anywhere, a first base above zero in
+    some rows, length nibbles 0 (derived from the width) to 15, and in some
+    rows a decreasing entry after which every base reads as 0x10000."""
+    rows = np.zeros((L, C, nb + 1), np.uint16)
+    for l in range(L):
+        for c in range(C):
+            bases = np.sort(rng.integers(0, 0x1000, size=nb)) * 16
+            if c % 3 == 0:
+                bases[0] = 0
+            nib = rng.integers(0, 16, size=nb)
+            nib[rng.random(nb) < 0.5] = 0
+            row = bases | nib
+            if c % 5 == 1 and nb > 2:
+                k = int(rng.integers(1, nb))
+                row[k] = (int(bases[k - 1]) // 2) & 0xFFF0
+            rows[l, c, :nb] = row
+    return rows.view(np.int16)
+
+
+@pytest.mark.parametrize("nb", [2, 3, 17, 40, 63])
+def test_decode_arbitrary_cdf_rows_vs_oracle(ops, nb):
+    """Random byte streams of random lengths (zero included) decoded under
+    hand-built CDF rows, bit-exact against the oracle."""
+    rng = np.random.default_rng(100 + nb)
+    L, C, T = 2, 64, 96
+    cdf = _arbitrary_cdf_rows(rng, L, C, nb)
+    lengths = rng.integers(0, 60, size=L * C)
+    lengths[::7] = 0
+    prefix = np.cumsum(lengths).astype(np.int32).reshape(L, C)
+    stream = rng.integers(0, 256, size=int(lengths.sum()), dtype=np.uint8)
+    want = oc.decode(cdf, stream, prefix, T)
+    out = torch.full((L, T, C), 0xEE, dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(torch.from_numpy(cdf).to(DEV), torch.from_numpy(stream).to(DEV),
+                            torch.from_numpy(prefix).to(DEV), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
