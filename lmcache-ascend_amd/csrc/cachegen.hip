@@ -450,46 +450,61 @@ __device__ __forceinline__ uint32_t win_word(const uint32_t *win, uint32_t last,
   return k >= 4 ? w : (w & ~(~0u >> (8 * k)));
 }
 
-// All 64 streams of the block lie in the window: L1/L2 lookups, window
-// dwords prefetched one refill ahead, and symbols transposed through LDS so
-// each lane stores one dword (4 channels of one token) per 4 tokens.
+// Keeps the bytes of a big-endian dword at stream offset q that lie before
+// the stream end `hi` (bytes at or past hi read as zero).
+__device__ __forceinline__ uint32_t clip_word(uint32_t w, uint32_t q, uint32_t hi) {
+  const int t = static_cast<int>(hi) - static_cast<int>(q);
+  const int k = t < 0 ? 0 : (t > 4 ? 4 : t);
+  return k >= 4 ? w : (w & ~(~0u >> (8 * k)));
+}
+
+// All 64 streams of the block lie in the window: L1/L2 lookups and symbols
+// transposed through LDS so each lane stores one dword (4 channels of one
+// token) per 4 tokens.  The bit window is refilled without branches: every
+// symbol reads the window dword at q (the next one to append) alongside its
+// L1 read, and the following symbol appends it when 32 bits or fewer are
+// left, so no LDS latency beyond the table lookup sits on the chain.
 __device__ __forceinline__ void decode_block_fast(const DecTables &tb, int T, int C,
                                                   const uint32_t *win, uint32_t win_last,
                                                   uint32_t lo, uint32_t hi, uint8_t *obuf,
                                                   uint8_t *__restrict__ out_blk) {
   const int lane = static_cast<int>(threadIdx.x);
   uint32_t q = lo & ~3u;
-  uint64_t buf = static_cast<uint64_t>(win_word(win, win_last, q, hi)) << 32;
-  q += 4;
+  uint64_t buf = static_cast<uint64_t>(clip_word(win[q >> 2], q, hi)) << 32;
   buf <<= 8 * (lo & 3u);
   int have = 32 - 8 * static_cast<int>(lo & 3u);
-  uint32_t nxt = win_word(win, win_last, q, hi);
   q += 4;
+  uint32_t nraw = win[(q < win_last ? q : win_last) >> 2];
+  auto step = [&]() -> int {
+    const bool refill = have <= 32;  // leaves more than 32 bits; codes are <= 15
+    const uint32_t w = refill ? clip_word(nraw, q, hi) : 0u;
+    buf |= static_cast<uint64_t>(w) << (refill ? 32 - have : 0);
+    have += refill ? 32 : 0;
+    q += refill ? 4u : 0u;
+    int s, len;
+    const uint32_t v = static_cast<uint32_t>(buf >> 48);
+    nraw = win[(q < win_last ? q : win_last) >> 2];
+    tb.lookup(v, s, len);
+    buf <<= len;
+    have -= len;
+    return s;
+  };
   // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
   uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
   const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
-  for (int t = 0; t < T; ++t) {
-    if (have <= 32) {  // leaves more than 32 bits; codes are <= 15
-      buf |= static_cast<uint64_t>(nxt) << (32 - have);
-      have += 32;
-      nxt = win_word(win, win_last, q, hi);
-      q += 4;
-    }
-    int s, len;
-    tb.lookup(static_cast<uint32_t>(buf >> 48), s, len);
-    obuf[(t & 3) * kDecLanes + lane] = static_cast<uint8_t>(s);
-    buf <<= len;
-    have -= len;
-    if ((t & 3) == 3) {
-      __syncthreads();
-      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
-      odst += step4;
-      __syncthreads();
-    }
-  }
-  if (T & 3) {
+  int t = 0;
+  for (; t + 4 <= T; t += 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
     __syncthreads();
-    if ((lane >> 4) < (T & 3)) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    odst += step4;
+    __syncthreads();
+  }
+  if (t < T) {
+    for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
+    __syncthreads();
+    if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
   }
 }
 
