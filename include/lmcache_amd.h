@@ -157,6 +157,100 @@ int lmc_reshape_and_cache_back_flash(const lmc_tensor *key_value,
                                      int32_t layer_idx, void *stream);
 
 /* ------------------------------------------------------------------------
+ * Sparse, direct and staged-batch single-layer transfers
+ * ------------------------------------------------------------------------ */
+
+/* Replaces sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:415-497;
+ * pybind csrc/pybind.cpp:381-387): retrieve only, for each i
+ * paged[slot_mapping_packed[i]] = LMC token selected_token_idx[i] of the
+ * single-layer buffer (layout as lmc_single_layer_kv_transfer).  Both index
+ * tensors are 1-D or both 2-D of the same shape; selected_token_idx is
+ * int32.  Entries with an out-of-range slot or token are skipped. */
+int lmc_sparse_single_layer_kv_transfer(
+    const lmc_tensor *lmc_key_value_cache, const lmc_tensor *caches,
+    int32_t n_caches, const lmc_tensor *slot_mapping_packed,
+    const lmc_tensor *selected_token_idx, int32_t kvcache_format,
+    int32_t token_major, int32_t vllm_two_major, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
+
+/* Replaces sparse_mla_dsa_batched_direct_kv_transfer and its _fast /
+ * _prepared forms (csrc/mem_kernels.cpp:584-1059; pybind csrc/pybind.cpp:
+ * 397-436): retrieve from memory objects reached through the device table
+ * chunk_ptrs (int64, one kernel-visible address per chunk).  Entry i moves
+ * token selected_token_idx[i] (chunk = token / chunk_size, n_c = min(
+ * chunk_size, total_tokens - chunk * chunk_size)) to slot
+ * slot_mapping_packed[i].  MLA/DSA chunks are stacked planes
+ * [K: n_c*kH | V: n_c*vH | DSA: n_c*dsaH] or, with lmc_host_interleaved,
+ * per-token [K | V | DSA] rows; MERGED/SEPARATE chunks have the layout of
+ * lmc_layout_sample ([n, 2, W] when token_major, else [2, n, W]).
+ * selected_token_counts (nullable, int32): entries form numel(counts) rows
+ * of equal width and row r holds counts[r * stride(0)] valid entries.
+ * validate_inputs adds the reference's argument checks. */
+int lmc_sparse_direct_kv_transfer(
+    const lmc_tensor *chunk_ptrs, const lmc_tensor *lmc_layout_sample,
+    const lmc_tensor *caches, int32_t n_caches,
+    const lmc_tensor *slot_mapping_packed, const lmc_tensor *selected_token_idx,
+    const lmc_tensor *selected_token_counts, int64_t chunk_size,
+    int64_t total_tokens, int32_t kvcache_format, int32_t token_major,
+    int32_t vllm_two_major, int64_t k_hidden_dims, int64_t v_hidden_dims,
+    int64_t dsa_hidden_dims, int32_t lmc_host_interleaved,
+    int32_t validate_inputs, void *stream);
+
+/* Replaces dense_mla_dsa_batched_direct_kv_transfer and its _fast /
+ * _prepared / group forms (csrc/mem_kernels.cpp:1131-1289; pybind
+ * csrc/pybind.cpp:441-472, 312-327), MLA/DSA formats: token g in
+ * [0, numel(slot_mapping_full)) belongs to chunk g / fixed_chunk_size, or
+ * (fixed_chunk_size == 0) to the chunk c with chunk_offsets[c] <= g <
+ * chunk_offsets[c] + chunk_sizes[c] (int32 device tables, ascending
+ * offsets); its rows move between that chunk and slot_mapping_full[g]
+ * (direction != 0: paged -> chunk).  Chunk layout as in
+ * lmc_sparse_direct_kv_transfer. */
+int lmc_dense_direct_kv_transfer(
+    const lmc_tensor *chunk_ptrs, const lmc_tensor *caches, int32_t n_caches,
+    const lmc_tensor *slot_mapping_full, const lmc_tensor *chunk_offsets,
+    const lmc_tensor *chunk_sizes, int64_t total_tokens,
+    int64_t fixed_chunk_size, int32_t kvcache_format, int32_t vllm_two_major,
+    int64_t k_hidden_dims, int64_t v_hidden_dims, int64_t dsa_hidden_dims,
+    int32_t lmc_host_interleaved, int32_t direction, int32_t validate_inputs,
+    void *stream);
+
+/* Replaces batched_fused_single_layer_kv_transfer (csrc/mem_kernels.cpp:
+ * 336-413; pybind csrc/pybind.cpp:373-380): a single-layer transfer between
+ * the paged caches and the device staging_cache, and one DMA copy per plane
+ * and chunk between staging tokens [chunk_offsets[i], + chunk_sizes[i]) and
+ * memory object lmc_tensors[i] (host chunk offsets and sizes; layouts as
+ * csrc/utils.cpp:500-733).  direction != 0: paged -> staging -> objects. */
+int lmc_batched_fused_single_layer_kv_transfer(
+    const lmc_tensor *lmc_tensors, int32_t n_chunks,
+    const lmc_tensor *staging_cache, const lmc_tensor *caches, int32_t n_caches,
+    const lmc_tensor *slot_mapping_full, const int64_t *chunk_offsets,
+    const int64_t *chunk_sizes, int32_t direction, int32_t kvcache_format,
+    int32_t token_major, int32_t vllm_two_major, int64_t k_hidden_dims,
+    int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
+
+/* Replaces batched_fused_sparse_single_layer_kv_transfer
+ * (csrc/mem_kernels.cpp:1291-1339; pybind csrc/pybind.cpp:388-396):
+ * objects -> staging, then lmc_sparse_single_layer_kv_transfer from the
+ * staging buffer. */
+int lmc_batched_fused_sparse_single_layer_kv_transfer(
+    const lmc_tensor *lmc_tensors, int32_t n_chunks,
+    const lmc_tensor *staging_cache, const lmc_tensor *caches, int32_t n_caches,
+    const lmc_tensor *slot_mapping_packed, const lmc_tensor *selected_token_idx,
+    const int64_t *chunk_offsets, const int64_t *chunk_sizes,
+    int32_t kvcache_format, int32_t token_major, int32_t vllm_two_major,
+    int64_t k_hidden_dims, int64_t v_hidden_dims, int64_t dsa_hidden_dims,
+    void *stream);
+
+/* The cache checks of prepare_sparse_direct_layer_state /
+ * prepare_sparse_direct_destination_state (csrc/utils.cpp:408-498,
+ * 903-966): LMC_ERR_VALUE with the reference's message on a bad format or
+ * cache tuple. */
+int lmc_check_kv_caches(const lmc_tensor *caches, int32_t n_caches,
+                        int32_t kvcache_format, int32_t vllm_two_major,
+                        int64_t k_hidden_dims, int64_t v_hidden_dims,
+                        int64_t dsa_hidden_dims);
+
+/* ------------------------------------------------------------------------
  * CacheGen codec
  * ------------------------------------------------------------------------ */
 

@@ -30,11 +30,7 @@
 // in-tree kernels and CPU substitutes skip negative slots
 // (csrc/graph/sparse_graph_kernel.cpp:45-48, tools/cpu_vllm_runtime.py:
 // 379-380); skipping is the superset.
-#include "common.h"
-
-#include <algorithm>
-#include <cstring>
-#include <vector>
+#include "kv_geom.h"
 
 namespace lmc {
 
@@ -55,37 +51,12 @@ namespace lmc {
 #ifndef LMC_KV_GRID_CAP
 #define LMC_KV_GRID_CAP 65535     // blocks per chunk (grid-stride beyond)
 #endif
-#ifndef LMC_KV_NT_LOADS
-#define LMC_KV_NT_LOADS 1         // streaming hint on loads of HBM copies
-#endif
-#ifndef LMC_KV_NT_STORES
-#define LMC_KV_NT_STORES 1        // streaming hint on stores of HBM copies
-#endif
 
-constexpr int kMaxPlanes = 3;
 constexpr int kMaxChunks = 64;
 constexpr int kThreads = LMC_KV_THREADS;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRowsPerWave = LMC_KV_ROWS_PER_WAVE;
 constexpr int kSegs = LMC_KV_SEGS;
-
-// Byte geometry of one plane (K, V or DSA) of a copy.
-struct PlaneDesc {
-  int64_t row_bytes;           // bytes per row
-  // LMCache side.  Offsets depend on the chunk's token count T (multi-layer
-  // memory objects are [kv, L, T, W]), so each is fixed + per_T * T.
-  int64_t lmc_off_fixed;
-  int64_t lmc_off_per_t;
-  int64_t lmc_layer_fixed;
-  int64_t lmc_layer_per_t;
-  int64_t lmc_token_stride;
-  // Paged side: row(s) = base + paged_off + (s / BS) * blk_stride
-  //                                        + (s % BS) * row_pitch
-  // or, with block_size == 0, base + paged_off + s * row_pitch.
-  int64_t paged_off;
-  int64_t blk_stride;
-  int64_t row_pitch;
-};
 
 struct CopyJob {
   PlaneDesc plane[kMaxPlanes];
@@ -109,24 +80,6 @@ struct ChunkList {
   int32_t tok_count[kMaxChunks];
 };
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-template <int VEC> struct VecOf;
-template <> struct VecOf<16> { using T = u32x4; };
-template <> struct VecOf<8> { using T = u32x2; };
-template <> struct VecOf<4> { using T = uint32_t; };
-template <> struct VecOf<2> { using T = uint16_t; };
-template <> struct VecOf<1> { using T = uint8_t; };
-
-template <typename T, bool NT> __device__ __forceinline__ T ld(const T *p) {
-  if constexpr (NT && LMC_KV_NT_LOADS) return __builtin_nontemporal_load(p);
-  else return *p;
-}
-template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
-  if constexpr (NT && LMC_KV_NT_STORES) __builtin_nontemporal_store(v, p);
-  else *p = v;
-}
 
 // Resolves row `row` of chunk `c` to (src, dst); returns the row's byte count,
 // or 0 when the slot is skipped.  All inputs are wave-uniform.
@@ -384,17 +337,6 @@ __global__ void __launch_bounds__(kThreads)
 
 namespace {
 
-int64_t gcd64(int64_t a, int64_t b) {
-  a = a < 0 ? -a : a;
-  b = b < 0 ? -b : b;
-  while (b) {
-    int64_t t = a % b;
-    a = b;
-    b = t;
-  }
-  return a;
-}
-
 // Largest access width (16/8/4/2/1 bytes) dividing every host-visible offset,
 // stride and address of the job.
 int pick_vec(const CopyJob &job, const ChunkList &chunks, int n_chunks) {
@@ -467,13 +409,6 @@ void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
 }
 
 
-bool nontemporal_enabled() {
-  static const bool on = [] {
-    const char *e = std::getenv("LMC_AMD_NONTEMPORAL");
-    return e == nullptr || e[0] != '0';
-  }();
-  return on;
-}
 
 // Launches one copy over `n` chunks (split into launches of kMaxChunks).
 // `host_lmc`: the LMCache side is page-locked host memory reached over PCIe;
@@ -522,15 +457,6 @@ void launch_copy(const CopyJob &job, const std::vector<uint64_t> &lmc_ptrs,
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
-const lmc_tensor &slots_of(const lmc_tensor *s) {
-  const lmc_tensor &t = deref(s, "slot_mapping");
-  check(t.ndim == 1, "slot_mapping must be 1-D");
-  check(t.dtype == LMC_I64 || t.dtype == LMC_I32,
-        "slot_mapping must be int64 or int32");
-  check(t.sizes[0] <= 1 || t.strides[0] == 1,
-        "slot_mapping must be contiguous");
-  return t;
-}
 
 // --- multi-layer planning (csrc/utils.cpp:29-86) ---------------------------
 
@@ -690,6 +616,26 @@ void run_multi_layer(const lmc_tensor *chunks, int n_chunks,
   launch_copy(g.job, lmc_ptrs, starts, counts, host_lmc, stream);
 }
 
+} // namespace
+
+bool nontemporal_enabled() {
+  static const bool on = [] {
+    const char *e = std::getenv("LMC_AMD_NONTEMPORAL");
+    return e == nullptr || e[0] != '0';
+  }();
+  return on;
+}
+
+const lmc_tensor &slots_of(const lmc_tensor *s) {
+  const lmc_tensor &t = deref(s, "slot_mapping");
+  check(t.ndim == 1, "slot_mapping must be 1-D");
+  check(t.dtype == LMC_I64 || t.dtype == LMC_I32,
+        "slot_mapping must be int64 or int32");
+  check(t.sizes[0] <= 1 || t.strides[0] == 1,
+        "slot_mapping must be contiguous");
+  return t;
+}
+
 // --- single-layer planning (csrc/utils.cpp:212-406, 903-966) ---------------
 
 void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt) {
@@ -726,32 +672,16 @@ void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt) {
   }
 }
 
-} // namespace
-
-void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
-                  const lmc_tensor *slots_t, bool direction, int fmt,
-                  bool token_major, bool two_major, int64_t kH, int64_t vH,
-                  int64_t dsaH, hipStream_t stream) {
+LayerGeom layer_geom(const lmc_tensor *caches, int n, int fmt, bool two_major,
+                     int64_t kH, int64_t vH, int64_t dsaH) {
   validate_vllm_caches(caches, n, fmt);
-  const lmc_tensor &lmc = deref(lmc_t, "lmc_key_value_cache");
-  const lmc_tensor &slots = slots_of(slots_t);
   const lmc_tensor &k = deref(&caches[0], "vllm_kv_caches[0]");
-  DeviceGuard guard(k.device);
-  const int64_t es = elem_size(k);
-  check(elem_size(lmc) == es, "LMC buffer and paged cache dtypes differ");
-  const int64_t T = slots.sizes[0];
-
-  CopyJob job;
-  std::memset(&job, 0, sizeof(job));
-  job.table = nullptr;
-  job.slots = kernel_ptr(slots);
-  job.slot_i32 = slots.dtype == LMC_I32;
-  job.n_layers = 1;
-  job.page2lmc = direction ? 1 : 0;
-
-  const bool mla_dsa = fmt == LMC_FMT_MLA_KV || fmt == LMC_FMT_DSA_KV ||
-                       fmt == LMC_FMT_MLA_LATENT || fmt == LMC_FMT_DSA_INDEX;
-  if (mla_dsa) {
+  LayerGeom g;
+  std::memset(&g, 0, sizeof(g));
+  g.device = k.device;
+  g.es = elem_size(k);
+  g.mla_dsa = is_mla_dsa(fmt);
+  if (g.mla_dsa) {
     // Hidden-dim defaults (csrc/utils.cpp:319-339).
     const lmc_tensor *v = nullptr, *dsa = nullptr;
     if (fmt != LMC_FMT_DSA_INDEX) v = &caches[1];
@@ -765,56 +695,41 @@ void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
       vH = 0;
     }
     const lmc_tensor *tens[kMaxPlanes] = {&k, v, dsa};
-    int64_t w[kMaxPlanes] = {kH, fmt == LMC_FMT_DSA_INDEX ? 0 : vH,
-                             fmt == LMC_FMT_DSA_KV ? dsaH : 0};
-    int64_t plane_elems = w[0] + w[1] + w[2];
-    check(plane_elems > 0, "MLA/DSA plane size must be positive");
-    // Stacked planes [K: N*kH | V: N*vH | DSA: N*dsaH] (csrc/utils.cpp:
-    // 222-224, 241-244, 350-357).
-    const int64_t N = numel(lmc) / plane_elems;
-    check(T <= N, "LMC buffer holds " + std::to_string(N) +
-                      " tokens, slot_mapping has " + std::to_string(T));
-    int planes = 0;
-    int64_t off = 0;
-    int64_t num_slots = INT64_MAX;
+    const int64_t w[kMaxPlanes] = {kH, fmt == LMC_FMT_DSA_INDEX ? 0 : vH,
+                                   fmt == LMC_FMT_DSA_KV ? dsaH : 0};
+    g.plane_elems = w[0] + w[1] + w[2];
+    check(g.plane_elems > 0, "MLA/DSA plane size must be positive");
+    int64_t pre = 0;
+    g.num_slots = INT64_MAX;
     for (int p = 0; p < kMaxPlanes; ++p) {
-      if (w[p] <= 0 || tens[p] == nullptr) { off += N * w[p]; continue; }
-      PlaneDesc &d = job.plane[planes];
-      d.row_bytes = w[p] * es;
-      d.lmc_off_fixed = off * es;
-      d.lmc_token_stride = w[p] * es;
-      d.paged_off = 0;
-      d.row_pitch = w[p] * es;
-      job.base[planes] = reinterpret_cast<uint64_t>(kernel_ptr(*tens[p]));
-      check(elem_size(*tens[p]) == es, "paged cache dtypes differ");
-      num_slots = std::min(num_slots, numel(*tens[p]) / w[p]);
-      off += N * w[p];
-      ++planes;
+      if (w[p] <= 0 || tens[p] == nullptr) {
+        pre += w[p];
+        continue;
+      }
+      const int q = g.n_planes++;
+      PlaneDesc &d = g.plane[q];
+      d.row_bytes = w[p] * g.es;
+      d.row_pitch = w[p] * g.es;
+      g.base[q] = reinterpret_cast<uint64_t>(kernel_ptr(*tens[p]));
+      g.width[q] = w[p];
+      g.prefix[q] = pre;
+      check(elem_size(*tens[p]) == g.es, "paged cache dtypes differ");
+      g.num_slots = std::min(g.num_slots, numel(*tens[p]) / w[p]);
+      pre += w[p];
     }
-    job.n_planes = planes;
-    job.block_size = 0;
-    job.num_slots = num_slots;
+    g.block_size = 0;
   } else {
     check(k.ndim >= 3, "paged cache must have at least 3 dims");
     const int64_t H = size(k, -2), D = size(k, -1), BS = size(k, -3);
     const int64_t W = H * D;
-    // LMC strides (csrc/utils.cpp:226-237): token-major [T, 2, W] or
-    // [2, T, W].
-    check(lmc.ndim >= 2, "LMC buffer must have at least 2 dims");
-    const int64_t tok_stride = token_major ? stride(lmc, 0) : stride(lmc, 1);
-    const int64_t val_off = token_major ? stride(lmc, 1) : stride(lmc, 0);
-    const int64_t lmc_need =
-        (T > 0 ? ((T - 1) * tok_stride + val_off + W) * es : 0);
-    check(lmc_need <= extent_bytes(lmc),
-          "LMC buffer is too small for " + std::to_string(T) + " tokens");
-    job.n_planes = 2;
-    job.block_size = static_cast<int32_t>(BS);
+    g.n_planes = 2;
+    g.plane_elems = 2 * W;
+    g.block_size = static_cast<int>(BS);
     for (int p = 0; p < 2; ++p) {
-      PlaneDesc &d = job.plane[p];
-      d.row_bytes = W * es;
-      d.lmc_off_fixed = p == 0 ? 0 : val_off * es;
-      d.lmc_token_stride = tok_stride * es;
-      d.row_pitch = W * es;
+      g.plane[p].row_bytes = W * g.es;
+      g.plane[p].row_pitch = W * g.es;
+      g.width[p] = W;
+      g.prefix[p] = p * W;
     }
     if (fmt == LMC_FMT_MERGED_KV) {
       // [2, NB, BS, H, D] (two-major) or [NB, 2, BS, H, D]
@@ -823,21 +738,80 @@ void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
       const int64_t blk = two_major ? stride(k, 1) : stride(k, 0);
       const int64_t voff = two_major ? stride(k, 0) : stride(k, 1);
       const int64_t NB = two_major ? size(k, 1) : size(k, 0);
-      job.base[0] = job.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(k));
-      job.plane[0].blk_stride = job.plane[1].blk_stride = blk * es;
-      job.plane[1].paged_off = voff * es;
-      job.num_slots = NB * BS;
+      g.base[0] = g.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(k));
+      g.plane[0].blk_stride = g.plane[1].blk_stride = blk * g.es;
+      g.plane[1].paged_off = voff * g.es;
+      g.num_slots = NB * BS;
     } else {
       // SEPARATE: (K, V) each [NB, BS, H, D] (csrc/utils.cpp:266-282).
       const lmc_tensor &v = deref(&caches[1], "vllm_kv_caches[1]");
-      check(elem_size(v) == es, "paged cache dtypes differ");
-      job.base[0] = reinterpret_cast<uint64_t>(kernel_ptr(k));
-      job.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(v));
-      job.plane[0].blk_stride = stride(k, 0) * es;
-      job.plane[1].blk_stride = stride(v, 0) * es;
-      job.num_slots = std::min(size(k, 0), size(v, 0)) * BS;
+      check(elem_size(v) == g.es, "paged cache dtypes differ");
+      g.base[0] = reinterpret_cast<uint64_t>(kernel_ptr(k));
+      g.base[1] = reinterpret_cast<uint64_t>(kernel_ptr(v));
+      g.plane[0].blk_stride = stride(k, 0) * g.es;
+      g.plane[1].blk_stride = stride(v, 0) * g.es;
+      g.num_slots = std::min(size(k, 0), size(v, 0)) * BS;
     }
   }
+  return g;
+}
+
+int64_t single_layer_lmc(const LayerGeom &g, const lmc_tensor &lmc,
+                         bool token_major, PlaneDesc *pl) {
+  check(elem_size(lmc) == g.es, "LMC buffer and paged cache dtypes differ");
+  if (g.mla_dsa) {
+    // Stacked planes [K: N*kH | V: N*vH | DSA: N*dsaH] (csrc/utils.cpp:
+    // 222-244, 350-357).
+    const int64_t N = numel(lmc) / g.plane_elems;
+    for (int p = 0; p < g.n_planes; ++p) {
+      pl[p].lmc_off_fixed = g.prefix[p] * N * g.es;
+      pl[p].lmc_token_stride = g.width[p] * g.es;
+    }
+    return N;
+  }
+  // Token-major [T, 2, W] or [2, T, W] by strides (csrc/utils.cpp:226-237).
+  check(lmc.ndim >= 2, "LMC buffer must have at least 2 dims");
+  const int64_t tok_stride = token_major ? stride(lmc, 0) : stride(lmc, 1);
+  const int64_t val_off = token_major ? stride(lmc, 1) : stride(lmc, 0);
+  for (int p = 0; p < 2; ++p) {
+    pl[p].lmc_off_fixed = p == 0 ? 0 : val_off * g.es;
+    pl[p].lmc_token_stride = tok_stride * g.es;
+  }
+  const int64_t room = extent_bytes(lmc) / g.es - val_off - g.width[0];
+  if (room < 0) return 0;
+  return tok_stride > 0 ? room / tok_stride + 1 : 1;
+}
+
+void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
+                  const lmc_tensor *slots_t, bool direction, int fmt,
+                  bool token_major, bool two_major, int64_t kH, int64_t vH,
+                  int64_t dsaH, hipStream_t stream) {
+  const LayerGeom g = layer_geom(caches, n, fmt, two_major, kH, vH, dsaH);
+  const lmc_tensor &lmc = deref(lmc_t, "lmc_key_value_cache");
+  const lmc_tensor &slots = slots_of(slots_t);
+  DeviceGuard guard(g.device);
+  const int64_t T = slots.sizes[0];
+
+  CopyJob job;
+  std::memset(&job, 0, sizeof(job));
+  job.table = nullptr;
+  job.slots = kernel_ptr(slots);
+  job.slot_i32 = slots.dtype == LMC_I32;
+  job.n_layers = 1;
+  job.page2lmc = direction ? 1 : 0;
+  job.n_planes = g.n_planes;
+  job.block_size = g.block_size;
+  job.num_slots = g.num_slots;
+  for (int p = 0; p < g.n_planes; ++p) {
+    job.plane[p] = g.plane[p];
+    job.base[p] = g.base[p];
+  }
+  const int64_t cap = single_layer_lmc(g, lmc, token_major, job.plane);
+  if (g.mla_dsa)
+    check(T <= cap, "LMC buffer holds " + std::to_string(cap) +
+                        " tokens, slot_mapping has " + std::to_string(T));
+  else
+    check(T <= cap, "LMC buffer is too small for " + std::to_string(T) + " tokens");
   if (T == 0) return;
   std::vector<uint64_t> lp{reinterpret_cast<uint64_t>(kernel_ptr(lmc))};
   std::vector<int64_t> st{0}, ct{T};

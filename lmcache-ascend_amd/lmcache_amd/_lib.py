@@ -60,6 +60,22 @@ SIGNATURES = {
     "lmc_single_layer_kv_transfer": [_T, _T, _i32, _T, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp],
     "lmc_load_and_reshape_flash": [_T, _T, _T, _T, _i32, _vp],
     "lmc_reshape_and_cache_back_flash": [_T, _T, _T, _T, _i32, _vp],
+    "lmc_sparse_single_layer_kv_transfer": [_T, _T, _i32, _T, _T, _i32, _i32, _i32, _i64, _i64, _i64, _vp],
+    "lmc_sparse_direct_kv_transfer": [
+        _T, _T, _T, _i32, _T, _T, _T, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _vp,
+    ],
+    "lmc_dense_direct_kv_transfer": [
+        _T, _T, _i32, _T, _T, _T, _i64, _i64, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp,
+    ],
+    "lmc_batched_fused_single_layer_kv_transfer": [
+        _T, _i32, _T, _T, _i32, _T, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, _i32, _i32, _i32,
+        _i64, _i64, _i64, _vp,
+    ],
+    "lmc_batched_fused_sparse_single_layer_kv_transfer": [
+        _T, _i32, _T, _T, _i32, _T, _T, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, _i32, _i32,
+        _i64, _i64, _i64, _vp,
+    ],
+    "lmc_check_kv_caches": [_T, _i32, _i32, _i32, _i64, _i64, _i64],
     "lmc_calculate_cdf": [_T, _i32, _T, _vp],
     "lmc_encode_fast_new": [_T, _T, _T, _T, _vp],
     "lmc_decode_fast_new": [_T, _T, _T, _T, _vp],

@@ -374,6 +374,404 @@ def rotary_embedding_k_fused(oldPositions, newPositions, key, headSize, cosSinCa
 
 
 # ---------------------------------------------------------------------------
+# Sparse, direct and staged-batch single-layer transfers
+# (csrc/mem_kernels.cpp:336-1339; csrc/pybind.cpp:45-340, 373-472)
+# ---------------------------------------------------------------------------
+
+_MLA_DSA = (3, 4, 5, 6)
+
+
+def _cache_array(caches):
+    arr = (_lib.LmcTensor * max(len(caches), 1))()
+    for i, c in enumerate(caches):
+        arr[i] = _desc(c)
+    return arr
+
+
+def _tensor_array(tensors):
+    return _cache_array(list(tensors))
+
+
+def _i64_array(values):
+    vals = [int(v) for v in values]
+    return (ctypes.c_int64 * max(len(vals), 1))(*vals)
+
+
+def _geom_desc(shape, strides, dtype) -> _lib.LmcTensor:
+    """Geometry-only descriptor (no data) of an LMC layout sample."""
+    return _lib.LmcTensor(0, _DTYPES[dtype], -1, len(shape), 0, _DIMS(*shape), _DIMS(*strides))
+
+
+def _check_caches(caches, fmt, two_major=False, kH=0, vH=0, dsaH=0) -> None:
+    arr = _cache_array(caches)
+    _run(_L.lmc_check_kv_caches(arr, len(caches), int(fmt), int(bool(two_major)), int(kH), int(vH), int(dsaH)))
+
+
+def _chunk_ptrs_for(lmc_tensors, device) -> torch.Tensor:
+    """Device int64 table of the memory objects' kernel-visible addresses
+    (csrc/mem_kernels.cpp:615-628)."""
+    ptrs = []
+    for t in lmc_tensors:
+        if t.is_cuda:
+            ptrs.append(t.data_ptr())
+            continue
+        p = get_device_ptr(t.data_ptr(), max(1, t.numel() * t.element_size()))
+        if p == 0:
+            raise RuntimeError("Unable to retrieve device ptr, is this a host registered pointer ?")
+        ptrs.append(p)
+    return torch.tensor(ptrs, dtype=torch.int64, device=device)
+
+
+def _mla_plane_elems(caches, fmt, kH, vH, dsaH) -> int:
+    """Elements of one token over all MLA/DSA planes, with the reference's
+    hidden-dim defaults (csrc/utils.cpp:310-339)."""
+    fmt = int(fmt)
+    k = caches[0]
+    if fmt == 6:
+        return int(dsaH) if dsaH > 0 else k.shape[-2] * k.shape[-1]
+    kH = int(kH) if kH > 0 else k.shape[-2] * k.shape[-1]
+    vH = int(vH) if vH > 0 else caches[1].shape[-2] * caches[1].shape[-1]
+    if fmt == 4:
+        return kH + vH + (int(dsaH) if dsaH > 0 else caches[2].shape[-2] * caches[2].shape[-1])
+    return kH + vH
+
+
+def _check_chunk_capacity(lmc_tensors, caches, fmt, kH, vH, dsaH, chunk_size, total_tokens) -> None:
+    """Memory object c must hold its min(chunk_size, total - c * chunk_size)
+    tokens (the kernels address them from the object's base)."""
+    if int(fmt) in _MLA_DSA:
+        per_token = _mla_plane_elems(caches, fmt, kH, vH, dsaH)
+        need = [min(chunk_size, total_tokens - c * chunk_size) * per_token for c in range(len(lmc_tensors))]
+    else:
+        need = [lmc_tensors[0].numel()] * len(lmc_tensors)
+    for c, (t, n) in enumerate(zip(lmc_tensors, need)):
+        if t.numel() < n:
+            raise RuntimeError(f"memory object {c} holds {t.numel()} elements, its chunk needs {n}")
+
+
+def _require_cpu_chunks(lmc_tensors, what: str) -> None:
+    if len(lmc_tensors) == 0:
+        raise RuntimeError("lmc_tensors must not be empty.")
+    for t in lmc_tensors:
+        if t.device.type != "cpu":
+            raise RuntimeError(what)
+
+
+def sparse_single_layer_kv_transfer(
+    lmc_key_value_cache, vllm_kv_caches, slot_mapping_packed, selected_token_idx, kvcache_format_raw,
+    token_major=False, vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0, dsa_hidden_dims=0,
+) -> None:
+    """Retrieve only: paged[slot_mapping_packed[i]] = LMC[selected_token_idx[i]]
+    (csrc/mem_kernels.cpp:415-497; tests/v1/test_mem_kernels.py:1445-1543)."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    arr = _cache_array(caches)
+    dev = _device_index(*(caches + [slot_mapping_packed]))
+    a, s, x = _desc(lmc_key_value_cache), _desc(slot_mapping_packed), _desc(selected_token_idx)
+    _run(
+        _L.lmc_sparse_single_layer_kv_transfer(
+            _ref(a), arr, len(caches), _ref(s), _ref(x), int(kvcache_format_raw), int(bool(token_major)),
+            int(bool(vllm_two_major)), int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims), _stream(dev),
+        )
+    )
+
+
+def batched_fused_single_layer_kv_transfer(
+    lmc_tensors, staging_cache, vllm_kv_caches, slot_mapping_full, chunk_offsets, chunk_sizes, direction,
+    kvcache_format_raw, token_major=False, vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0,
+    dsa_hidden_dims=0,
+) -> None:
+    """Single-layer copy through `staging_cache` plus one DMA copy per chunk
+    and plane (csrc/mem_kernels.cpp:336-413; tests/v1/test_mem_kernels.py:
+    791-1062).  direction True: paged -> staging -> lmc_tensors."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    arr = _cache_array(caches)
+    objs = _tensor_array(lmc_tensors)
+    if len(chunk_offsets) != len(lmc_tensors) or len(chunk_sizes) != len(lmc_tensors):
+        raise RuntimeError("chunk_offsets and chunk_sizes need one entry per memory object")
+    dev = _device_index(*(caches + [slot_mapping_full, staging_cache]))
+    st, s = _desc(staging_cache), _desc(slot_mapping_full)
+    _run(
+        _L.lmc_batched_fused_single_layer_kv_transfer(
+            objs, len(lmc_tensors), _ref(st), arr, len(caches), _ref(s), _i64_array(chunk_offsets),
+            _i64_array(chunk_sizes), int(bool(direction)), int(kvcache_format_raw), int(bool(token_major)),
+            int(bool(vllm_two_major)), int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims), _stream(dev),
+        )
+    )
+
+
+def batched_fused_sparse_single_layer_kv_transfer(
+    lmc_tensors, staging_cache, vllm_kv_caches, slot_mapping_packed, selected_token_idx, chunk_offsets,
+    chunk_sizes, kvcache_format_raw, token_major=False, vllm_two_major=False, k_hidden_dims=0,
+    v_hidden_dims=0, dsa_hidden_dims=0, sparse_indices_cpu=None,
+) -> None:
+    """lmc_tensors -> staging, then sparse_single_layer_kv_transfer from the
+    staging buffer (csrc/mem_kernels.cpp:1291-1339).  `sparse_indices_cpu`
+    only steers the reference's choice of per-token copies; every chunk is
+    staged whole here."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    arr = _cache_array(caches)
+    objs = _tensor_array(lmc_tensors)
+    if len(chunk_offsets) != len(lmc_tensors) or len(chunk_sizes) != len(lmc_tensors):
+        raise RuntimeError("chunk_offsets and chunk_sizes need one entry per memory object")
+    dev = _device_index(*(caches + [slot_mapping_packed, staging_cache]))
+    st, s, x = _desc(staging_cache), _desc(slot_mapping_packed), _desc(selected_token_idx)
+    _run(
+        _L.lmc_batched_fused_sparse_single_layer_kv_transfer(
+            objs, len(lmc_tensors), _ref(st), arr, len(caches), _ref(s), _ref(x), _i64_array(chunk_offsets),
+            _i64_array(chunk_sizes), int(kvcache_format_raw), int(bool(token_major)), int(bool(vllm_two_major)),
+            int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims), _stream(dev),
+        )
+    )
+
+
+class SparseDirectLayerState:
+    """prepare_sparse_direct_layer_state's result (csrc/utils.cpp:408-423):
+    one layer's caches and LMC layout, checked once."""
+
+    __slots__ = ("caches", "kvcache_format", "token_major", "vllm_two_major", "k_hidden_dims",
+                 "v_hidden_dims", "dsa_hidden_dims", "layout", "lmc_num_tokens")
+
+
+class SparseDirectDestinationState:
+    """prepare_sparse_direct_destination_state's result (csrc/utils.cpp:
+    425-498): one layer's MLA/DSA caches, checked once."""
+
+    __slots__ = ("caches", "kvcache_format", "k_hidden_dims", "v_hidden_dims", "dsa_hidden_dims")
+
+
+def prepare_sparse_direct_layer_state(
+    lmc_layout_sample, vllm_kv_caches, slot_mapping_ref, token_major, vllm_two_major, kvcache_format_raw,
+    k_hidden_dims, v_hidden_dims, dsa_hidden_dims, lmc_num_tokens,
+) -> SparseDirectLayerState:
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
+    st = SparseDirectLayerState()
+    st.caches = tuple(caches)
+    st.kvcache_format = int(kvcache_format_raw)
+    st.token_major = bool(token_major)
+    st.vllm_two_major = bool(vllm_two_major)
+    st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims = int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims)
+    st.layout = (tuple(lmc_layout_sample.shape), tuple(lmc_layout_sample.stride()), lmc_layout_sample.dtype)
+    st.lmc_num_tokens = int(lmc_num_tokens)
+    return st
+
+
+def prepare_sparse_direct_destination_state(
+    vllm_kv_caches, slot_mapping_ref, kvcache_format_raw, k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
+) -> SparseDirectDestinationState:
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    _check_caches(caches, kvcache_format_raw, False, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
+    if int(kvcache_format_raw) not in _MLA_DSA:
+        raise RuntimeError("Prepared sparse destination state only supports MLA/DSA formats.")
+    st = SparseDirectDestinationState()
+    st.caches = tuple(caches)
+    st.kvcache_format = int(kvcache_format_raw)
+    st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims = int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims)
+    return st
+
+
+def _sparse_direct(caches, fmt, token_major, two_major, kH, vH, dsaH, layout, slot_mapping_packed,
+                   selected_token_idx, chunk_ptrs, counts, chunk_size, total_tokens, interleaved, validate):
+    arr = _cache_array(caches)
+    dev = _device_index(*(list(caches) + [slot_mapping_packed]))
+    p, s, x = _desc(chunk_ptrs), _desc(slot_mapping_packed), _desc(selected_token_idx)
+    lay = _geom_desc(*layout) if layout is not None else None
+    cnt = _desc(counts) if counts is not None else None
+    _run(
+        _L.lmc_sparse_direct_kv_transfer(
+            _ref(p), _ref(lay) if lay is not None else None, arr, len(caches), _ref(s), _ref(x),
+            _ref(cnt) if cnt is not None else None, int(chunk_size), int(total_tokens), int(fmt),
+            int(bool(token_major)), int(bool(two_major)), int(kH), int(vH), int(dsaH), int(bool(interleaved)),
+            int(bool(validate)), _stream(dev),
+        )
+    )
+
+
+def sparse_mla_dsa_batched_direct_kv_transfer(
+    lmc_tensors, vllm_kv_caches, slot_mapping_packed, selected_token_idx, chunk_size, total_tokens,
+    kvcache_format_raw, token_major=False, vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0,
+    dsa_hidden_dims=0, lmc_host_interleaved=False, chunk_ptrs_npu=None, selected_token_counts=None,
+) -> None:
+    """Retrieve selected tokens straight from pinned memory objects
+    (csrc/mem_kernels.cpp:584-672; tools/cpu_vllm_runtime.py:288-343)."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
+    if int(chunk_size) <= 0:
+        raise RuntimeError("chunk_size must be positive.")
+    if int(total_tokens) <= 0:
+        raise RuntimeError("total_tokens must be positive.")
+    _require_cpu_chunks(lmc_tensors, "Direct sparse retrieve requires CPU pinned memory objects.")
+    _check_chunk_capacity(lmc_tensors, caches, kvcache_format_raw, k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
+                          int(chunk_size), int(total_tokens))
+    if selected_token_idx.numel() == 0:
+        return
+    if chunk_ptrs_npu is None or chunk_ptrs_npu.numel() != len(lmc_tensors):
+        chunk_ptrs_npu = _chunk_ptrs_for(lmc_tensors, slot_mapping_packed.device)
+    s0 = lmc_tensors[0]
+    _sparse_direct(caches, kvcache_format_raw, token_major, vllm_two_major, k_hidden_dims, v_hidden_dims,
+                   dsa_hidden_dims, (tuple(s0.shape), tuple(s0.stride()), s0.dtype), slot_mapping_packed,
+                   selected_token_idx, chunk_ptrs_npu, selected_token_counts, chunk_size, total_tokens,
+                   lmc_host_interleaved, True)
+
+
+def sparse_mla_dsa_batched_direct_kv_transfer_fast(
+    layer_state, slot_mapping_packed, selected_token_idx, chunk_ptrs_npu, chunk_size, total_tokens,
+    lmc_host_interleaved, validate_inputs=False, selected_token_counts=None,
+) -> None:
+    """csrc/mem_kernels.cpp:674-738."""
+    st = layer_state
+    if selected_token_idx.numel() == 0 and not validate_inputs:
+        return
+    _sparse_direct(st.caches, st.kvcache_format, st.token_major, st.vllm_two_major, st.k_hidden_dims,
+                   st.v_hidden_dims, st.dsa_hidden_dims, st.layout, slot_mapping_packed, selected_token_idx,
+                   chunk_ptrs_npu, selected_token_counts, chunk_size, total_tokens, lmc_host_interleaved,
+                   validate_inputs)
+
+
+def sparse_mla_dsa_batched_direct_kv_transfer_prepared(
+    destination_state, slot_mapping_packed, selected_token_idx, chunk_ptrs_npu, chunk_size, total_tokens,
+    lmc_host_interleaved, selected_token_counts=None, diagnostic_layer_id=-1,
+) -> None:
+    """csrc/mem_kernels.cpp:833-949 (the diagnostic timing is not kept)."""
+    st = destination_state
+    if selected_token_idx.numel() == 0:
+        return
+    _sparse_direct(st.caches, st.kvcache_format, False, False, st.k_hidden_dims, st.v_hidden_dims,
+                   st.dsa_hidden_dims, None, slot_mapping_packed, selected_token_idx, chunk_ptrs_npu,
+                   selected_token_counts, chunk_size, total_tokens, lmc_host_interleaved, False)
+
+
+def _dense_direct(caches, fmt, kH, vH, dsaH, slot_mapping_full, chunk_ptrs, chunk_offsets, chunk_sizes,
+                  total_tokens, fixed_chunk_size, interleaved, direction, validate, two_major=False):
+    arr = _cache_array(caches)
+    dev = _device_index(*(list(caches) + [slot_mapping_full]))
+    p, s = _desc(chunk_ptrs), _desc(slot_mapping_full)
+    o, z = _desc(chunk_offsets), _desc(chunk_sizes)
+    _run(
+        _L.lmc_dense_direct_kv_transfer(
+            _ref(p), arr, len(caches), _ref(s), _ref(o), _ref(z), int(total_tokens), int(fixed_chunk_size),
+            int(fmt), int(bool(two_major)), int(kH), int(vH), int(dsaH), int(bool(interleaved)),
+            int(bool(direction)), int(bool(validate)), _stream(dev),
+        )
+    )
+
+
+def dense_mla_dsa_batched_direct_kv_transfer(
+    lmc_tensors, vllm_kv_caches, slot_mapping_full, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+    kvcache_format_raw, token_major=False, vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0,
+    dsa_hidden_dims=0, lmc_host_interleaved=False, direction=False, chunk_ptrs_npu=None, fixed_chunk_size=0,
+) -> None:
+    """Every token of each memory object, either direction
+    (csrc/mem_kernels.cpp:1131-1186; tools/cpu_vllm_runtime.py:353-411)."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
+    if int(kvcache_format_raw) not in _MLA_DSA:
+        raise RuntimeError("Dense direct transfer only supports MLA/DSA formats.")
+    _require_cpu_chunks(lmc_tensors, "Dense direct transfer requires CPU pinned memory objects.")
+    if int(fixed_chunk_size) > 0:
+        _check_chunk_capacity(lmc_tensors, caches, kvcache_format_raw, k_hidden_dims, v_hidden_dims,
+                              dsa_hidden_dims, int(fixed_chunk_size), int(total_tokens))
+    if chunk_ptrs_npu is None or chunk_ptrs_npu.numel() != len(lmc_tensors):
+        chunk_ptrs_npu = _chunk_ptrs_for(lmc_tensors, slot_mapping_full.device)
+    _dense_direct(caches, kvcache_format_raw, k_hidden_dims, v_hidden_dims, dsa_hidden_dims, slot_mapping_full,
+                  chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens, fixed_chunk_size,
+                  lmc_host_interleaved, direction, True, vllm_two_major)
+
+
+def dense_mla_dsa_batched_direct_kv_transfer_fast(
+    layer_state, slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+    lmc_host_interleaved, direction, validate_inputs=False, fixed_chunk_size=0,
+) -> None:
+    """csrc/mem_kernels.cpp:1188-1231."""
+    st = layer_state
+    _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
+                  slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+                  fixed_chunk_size, lmc_host_interleaved, direction, validate_inputs, st.vllm_two_major)
+
+
+def dense_mla_dsa_batched_direct_kv_transfer_prepared(
+    destination_state, slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+    lmc_host_interleaved, validate_inputs=False, fixed_chunk_size=0,
+) -> None:
+    """Retrieve (memory objects -> paged), csrc/mem_kernels.cpp:1233-1277."""
+    st = destination_state
+    _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
+                  slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+                  fixed_chunk_size, lmc_host_interleaved, False, validate_inputs)
+
+
+def _dense_group(layer_states, slot_mapping_full, layer_chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu,
+                 total_tokens, lmc_host_interleaved, direction, validate_inputs, fixed_chunk_size):
+    """One dense direct transfer per layer, layer l using row l of the
+    [layers, chunks] pointer table (csrc/mem_kernels.cpp:1279-1339)."""
+    if len(layer_states) == 0:
+        raise RuntimeError("layer_states must not be empty.")
+    if layer_chunk_ptrs_npu.dim() != 2:
+        raise RuntimeError("layer_chunk_ptrs_npu must be 2D [layers, chunks].")
+    if layer_chunk_ptrs_npu.size(0) != len(layer_states):
+        raise RuntimeError("layer pointer table row count must match layer_states.")
+    if layer_chunk_ptrs_npu.size(1) <= 0:
+        raise RuntimeError("layer pointer table must contain at least one chunk.")
+    if not layer_chunk_ptrs_npu.is_contiguous():
+        raise RuntimeError("layer_chunk_ptrs_npu must be contiguous.")
+    for layer_id, st in enumerate(layer_states):
+        _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
+                      slot_mapping_full, layer_chunk_ptrs_npu[layer_id], chunk_offsets_npu, chunk_sizes_npu,
+                      total_tokens, fixed_chunk_size, lmc_host_interleaved, direction,
+                      validate_inputs and layer_id == 0, st.vllm_two_major)
+
+
+def dense_mla_dsa_group_direct_kv_transfer_fast(
+    layer_states, layer_tensors, slot_mapping_full, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+    lmc_host_interleaved, direction, validate_inputs=False, fixed_chunk_size=0,
+):
+    """Dense direct transfer of several layers into registered host memory
+    objects; returns (host_pointer_rows, layer_chunk_ptrs_npu)
+    (csrc/pybind.cpp:187-240)."""
+    layer_states = list(layer_states)
+    if len(layer_states) == 0:
+        raise RuntimeError("layer_states must not be empty.")
+    if len(layer_tensors) != len(layer_states):
+        raise RuntimeError("layer tensor rows must match layer states.")
+    rows, flat, num_chunks = [], [], None
+    for layer_id, tensors in enumerate(layer_tensors):
+        if num_chunks is None:
+            num_chunks = len(tensors)
+            if num_chunks <= 0:
+                raise RuntimeError("each group store layer must contain at least one chunk.")
+        if len(tensors) != num_chunks:
+            raise RuntimeError("all group store layers must have the same chunk count.")
+        row = []
+        for chunk_id, t in enumerate(tensors):
+            if t.device.type != "cpu":
+                raise RuntimeError("group direct store requires CPU destination tensors.")
+            p = get_device_ptr(t.data_ptr())
+            if p == 0:
+                raise RuntimeError(
+                    "group direct store destination tensor is not registered: "
+                    f"layer={layer_id}, chunk={chunk_id}"
+                )
+            row.append(p)
+            flat.append(p)
+        rows.append(row)
+    table = torch.tensor(flat, dtype=torch.int64, device=slot_mapping_full.device).reshape(
+        len(layer_states), num_chunks
+    )
+    _dense_group(layer_states, slot_mapping_full, table, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
+                 lmc_host_interleaved, direction, validate_inputs, fixed_chunk_size)
+    return rows, table
+
+
+def dense_mla_dsa_group_direct_kv_transfer_prepared(
+    objects, slots, pointers, offsets, sizes, tokens, interleaved, validate, fixed_chunk_size,
+) -> None:
+    """Store (paged -> memory objects) of several layers through a prepared
+    [layers, chunks] pointer table (csrc/pybind.cpp:312-327)."""
+    _dense_group(list(objects), slots, pointers, offsets, sizes, tokens, interleaved, True, validate,
+                 fixed_chunk_size)
+
+
+# ---------------------------------------------------------------------------
 # Pinned host memory
 # ---------------------------------------------------------------------------
 

@@ -127,18 +127,14 @@ class TensorBytes:
         return n
 
 
-def single_layer_kv_transfer(lmc: TensorBytes, caches: List[TensorBytes], slots: np.ndarray,
-                             direction: bool, fmt: int, token_major: bool = False,
-                             vllm_two_major: bool = False, kH: int = 0, vH: int = 0,
-                             dsaH: int = 0) -> None:
-    """single_layer_kv_transfer (csrc/mem_kernels.cpp:265-334), in place.
-
-    Strides follow csrc/utils.cpp:212-285; MLA/DSA hidden-dim defaults and the
-    stacked-plane LMC layout follow csrc/utils.cpp:310-357.
-    """
+def _layer_planes(caches: List[TensorBytes], fmt: int, vllm_two_major: bool, kH: int, vH: int,
+                  dsaH: int):
+    """Paged side of one layer (csrc/utils.cpp:212-406): a list of
+    (cache, row bytes, paged offset, row pitch, block stride, width,
+    prefix) per plane, plus num_slots, block_size and the LMC token width
+    (sum of plane widths)."""
     es = caches[0].es
-    T = int(slots.shape[0])
-    rows = []  # (lmc byte offsets[T], paged buffer, paged byte offsets[T], row bytes)
+    planes = []
     if fmt in (MLA_KV, DSA_KV, MLA_LATENT, DSA_INDEX):
         k = caches[0]
         v = caches[1] if fmt != DSA_INDEX else None
@@ -153,55 +149,225 @@ def single_layer_kv_transfer(lmc: TensorBytes, caches: List[TensorBytes], slots:
             kH = dsaH if dsaH > 0 else k.shape[-2] * k.shape[-1]
             vH = 0
         widths = [kH, vH if fmt != DSA_INDEX else 0, dsaH if fmt == DSA_KV else 0]
-        tensors = [k, v, dsa]
-        plane_elems = sum(widths)
-        N = lmc.numel // plane_elems
-        assert T <= N, "LMC buffer too small"
-        off = 0
-        num_slots = None
-        for w, tb in zip(widths, tensors):
+        num_slots, pre = None, 0
+        for w, tb in zip(widths, [k, v, dsa]):
             if w > 0 and tb is not None:
-                t = np.arange(T, dtype=np.int64)
-                lmc_off = (off + t * w) * es
-                rows.append((lmc_off, tb, w * es, 0, w * es, 0))
+                planes.append((tb, w * es, 0, w * es, 0, w, pre))
                 ns = tb.numel // w
                 num_slots = ns if num_slots is None else min(num_slots, ns)
-            off += N * w
-        block_size = 0
+            pre += w
+        return planes, num_slots, 0, sum(widths)
+    k = caches[0]
+    H, D, BS = k.shape[-2], k.shape[-1], k.shape[-3]
+    W = H * D
+    if fmt == MERGED_KV:
+        blk = k.strides[1] if vllm_two_major else k.strides[0]
+        voff = k.strides[0] if vllm_two_major else k.strides[1]
+        NB = k.shape[1] if vllm_two_major else k.shape[0]
+        planes = [(k, W * es, 0, W * es, blk * es, W, 0), (k, W * es, voff * es, W * es, blk * es, W, W)]
+        return planes, NB * BS, BS, 2 * W
+    v = caches[1]
+    planes = [(k, W * es, 0, W * es, k.strides[0] * es, W, 0),
+              (v, W * es, 0, W * es, v.strides[0] * es, W, W)]
+    return planes, min(k.shape[0], v.shape[0]) * BS, BS, 2 * W
+
+
+def _single_layer_lmc(lmc: TensorBytes, planes, plane_elems: int, mla_dsa: bool, token_major: bool):
+    """LMC side of a single-layer buffer: (byte offset of plane p's token 0,
+    byte stride per token) per plane, and the tokens it holds
+    (csrc/utils.cpp:222-244, 350-357)."""
+    es = lmc.es
+    if mla_dsa:
+        N = lmc.numel // plane_elems
+        return [(pre * N * es, w * es) for (_, _, _, _, _, w, pre) in planes], N
+    if token_major:
+        tok_stride, val_off = lmc.strides[0], lmc.strides[1]
     else:
-        k = caches[0]
-        H, D, BS = k.shape[-2], k.shape[-1], k.shape[-3]
-        W = H * D
-        if token_major:
-            tok_stride, val_off = lmc.strides[0], lmc.strides[1]
-        else:
-            tok_stride, val_off = lmc.strides[1], lmc.strides[0]
-        t = np.arange(T, dtype=np.int64)
-        if fmt == MERGED_KV:
-            blk = k.strides[1] if vllm_two_major else k.strides[0]
-            voff = k.strides[0] if vllm_two_major else k.strides[1]
-            NB = k.shape[1] if vllm_two_major else k.shape[0]
-            rows.append((t * tok_stride * es, k, W * es, 0, W * es, blk * es))
-            rows.append(((t * tok_stride + val_off) * es, k, W * es, voff * es, W * es, blk * es))
-            num_slots = NB * BS
-        else:
-            v = caches[1]
-            rows.append((t * tok_stride * es, k, W * es, 0, W * es, k.strides[0] * es))
-            rows.append(((t * tok_stride + val_off) * es, v, W * es, 0, W * es, v.strides[0] * es))
-            num_slots = min(k.shape[0], v.shape[0]) * BS
-        block_size = BS
+        tok_stride, val_off = lmc.strides[1], lmc.strides[0]
+    N = lmc.shape[0] if token_major else lmc.shape[1]
+    return [(0, tok_stride * es), (val_off * es, tok_stride * es)], N
+
+
+def _paged_offsets(slot: np.ndarray, plane, block_size: int) -> np.ndarray:
+    _, _, poff, pitch, blk, _, _ = plane
+    if block_size:
+        return poff + (slot // block_size) * blk + (slot % block_size) * pitch
+    return poff + slot * pitch
+
+
+def single_layer_kv_transfer(lmc: TensorBytes, caches: List[TensorBytes], slots: np.ndarray,
+                             direction: bool, fmt: int, token_major: bool = False,
+                             vllm_two_major: bool = False, kH: int = 0, vH: int = 0,
+                             dsaH: int = 0) -> None:
+    """single_layer_kv_transfer (csrc/mem_kernels.cpp:265-334), in place.
+
+    Strides follow csrc/utils.cpp:212-285; MLA/DSA hidden-dim defaults and the
+    stacked-plane LMC layout follow csrc/utils.cpp:310-357.
+    """
+    T = int(slots.shape[0])
+    mla = fmt in (MLA_KV, DSA_KV, MLA_LATENT, DSA_INDEX)
+    planes, num_slots, block_size, pe = _layer_planes(caches, fmt, vllm_two_major, kH, vH, dsaH)
+    lmc_geo, N = _single_layer_lmc(lmc, planes, pe, mla, token_major)
+    assert T <= N, "LMC buffer too small"
     valid = (slots >= 0) & (slots < num_slots)
     s = slots[valid].astype(np.int64)
-    for lmc_off, tb, rb, poff, pitch, blk in rows:
-        if block_size:
-            p_off = poff + (s // block_size) * blk + (s % block_size) * pitch
-        else:
-            p_off = poff + s * pitch
-        l_off = lmc_off[valid]
+    t = np.nonzero(valid)[0].astype(np.int64)
+    for plane, (l0, lstride) in zip(planes, lmc_geo):
+        tb, rb = plane[0], plane[1]
+        p_off = _paged_offsets(s, plane, block_size)
+        l_off = l0 + t * lstride
         if direction:
             _scatter_rows(lmc.data, l_off, _gather_rows(tb.data, p_off, rb))
         else:
             _scatter_rows(tb.data, p_off, _gather_rows(lmc.data, l_off, rb))
+
+
+def sparse_single_layer_kv_transfer(lmc: TensorBytes, caches: List[TensorBytes],
+                                    slots_packed: np.ndarray, selected: np.ndarray, fmt: int,
+                                    token_major: bool = False, vllm_two_major: bool = False,
+                                    kH: int = 0, vH: int = 0, dsaH: int = 0) -> None:
+    """sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:415-497;
+    tests/v1/test_mem_kernels.py:1445-1543): for each i, paged row
+    slots_packed[i] <- LMC token selected[i]; entries whose slot or token is
+    out of range are skipped."""
+    mla = fmt in (MLA_KV, DSA_KV, MLA_LATENT, DSA_INDEX)
+    planes, num_slots, block_size, pe = _layer_planes(caches, fmt, vllm_two_major, kH, vH, dsaH)
+    lmc_geo, N = _single_layer_lmc(lmc, planes, pe, mla, token_major)
+    slots_packed = slots_packed.reshape(-1).astype(np.int64)
+    selected = selected.reshape(-1).astype(np.int64)
+    valid = (slots_packed >= 0) & (slots_packed < num_slots) & (selected >= 0) & (selected < N)
+    s, t = slots_packed[valid], selected[valid]
+    for plane, (l0, lstride) in zip(planes, lmc_geo):
+        _scatter_rows(plane[0].data, _paged_offsets(s, plane, block_size),
+                      _gather_rows(lmc.data, l0 + t * lstride, plane[1]))
+
+
+def _chunk_row_offset(plane, pe: int, n_c: int, t: int, es: int, interleaved: bool) -> int:
+    """Byte offset of token t of plane `plane` inside an MLA/DSA memory
+    object of n_c tokens: stacked planes [K: n_c*kH | V: n_c*vH | DSA] or
+    per-token [K | V | DSA] rows (tools/cpu_vllm_runtime.py:322-330,
+    366-373)."""
+    w, pre = plane[5], plane[6]
+    if interleaved:
+        return (t * pe + pre) * es
+    return (pre * n_c + t * w) * es
+
+
+def dense_direct_kv_transfer(chunks: Sequence[np.ndarray], caches: List[TensorBytes],
+                             slots: np.ndarray, total_tokens: int, chunk_offsets, chunk_sizes,
+                             fixed_chunk_size: int, fmt: int, kH: int = 0, vH: int = 0,
+                             dsaH: int = 0, interleaved: bool = False,
+                             direction: bool = False) -> None:
+    """dense_mla_dsa_batched_direct_kv_transfer, following the reference's
+    CPU restatement (tools/cpu_vllm_runtime.py:353-411): chunk c covers
+    tokens [start, start + count) of slot_mapping (start = c * fixed or
+    chunk_offsets[c]); direction True: paged -> chunk."""
+    planes, num_slots, block_size, pe = _layer_planes(caches, fmt, False, kH, vH, dsaH)
+    es = caches[0].es
+    slots = slots.astype(np.int64)
+    for c, buf in enumerate(chunks):
+        if fixed_chunk_size:
+            start = c * fixed_chunk_size
+            count = min(fixed_chunk_size, total_tokens - start)
+        else:
+            start, count = int(chunk_offsets[c]), int(chunk_sizes[c])
+        for t in range(count):
+            g = start + t
+            if g >= slots.shape[0]:
+                break
+            s = int(slots[g])
+            if s < 0 or s >= num_slots:
+                continue
+            for plane in planes:
+                rb = plane[1]
+                po = int(_paged_offsets(np.int64(s), plane, block_size))
+                lo = _chunk_row_offset(plane, pe, count, t, es, interleaved)
+                if direction:
+                    buf[lo: lo + rb] = plane[0].data[po: po + rb]
+                else:
+                    plane[0].data[po: po + rb] = buf[lo: lo + rb]
+
+
+def sparse_direct_kv_transfer(chunks: Sequence[np.ndarray], caches: List[TensorBytes],
+                              slots_packed: np.ndarray, selected: np.ndarray, chunk_size: int,
+                              total_tokens: int, fmt: int, kH: int = 0, vH: int = 0,
+                              dsaH: int = 0, interleaved: bool = False, counts=None,
+                              layout: TensorBytes = None, token_major: bool = False,
+                              vllm_two_major: bool = False) -> None:
+    """sparse_mla_dsa_batched_direct_kv_transfer, following the reference's
+    CPU restatement (tools/cpu_vllm_runtime.py:288-343): entry i moves token
+    selected[i] (chunk selected[i] // chunk_size, n_c = min(chunk_size,
+    total_tokens - chunk * chunk_size)) into paged row slots_packed[i].
+    `counts` (csrc/mem_kernels.cpp:641-649): the entries form len(counts)
+    rows of equal width; only the first counts[r] of row r are valid.
+    MERGED/SEPARATE memory objects have the layout of `layout` (shape and
+    strides of the first chunk)."""
+    mla = fmt in (MLA_KV, DSA_KV, MLA_LATENT, DSA_INDEX)
+    planes, num_slots, block_size, pe = _layer_planes(caches, fmt, vllm_two_major, kH, vH, dsaH)
+    es = caches[0].es
+    slots_packed = slots_packed.reshape(-1).astype(np.int64)
+    selected = selected.reshape(-1).astype(np.int64)
+    n = selected.shape[0]
+    row_w = n // len(counts) if counts is not None else 0
+    if not mla:
+        lmc_geo, _ = _single_layer_lmc(layout, planes, pe, False, token_major)
+    for i in range(n):
+        if counts is not None:
+            r = i // row_w
+            if r >= len(counts) or i - r * row_w >= int(counts[r]):
+                continue
+        tok, s = int(selected[i]), int(slots_packed[i])
+        if tok < 0 or tok >= total_tokens or s < 0 or s >= num_slots:
+            continue
+        c = tok // chunk_size
+        if c >= len(chunks):
+            continue
+        t = tok - c * chunk_size
+        n_c = min(chunk_size, total_tokens - c * chunk_size)
+        for q, plane in enumerate(planes):
+            rb = plane[1]
+            po = int(_paged_offsets(np.int64(s), plane, block_size))
+            if mla:
+                lo = _chunk_row_offset(plane, pe, n_c, t, es, interleaved)
+            else:
+                lo = lmc_geo[q][0] + t * lmc_geo[q][1]
+            plane[0].data[po: po + rb] = chunks[c][lo: lo + rb]
+
+
+def stage_chunks(staging: TensorBytes, caches: List[TensorBytes], objs: Sequence[TensorBytes],
+                 offsets, sizes, fmt: int, token_major: bool, to_objects: bool,
+                 vllm_two_major: bool = False, kH: int = 0, vH: int = 0, dsaH: int = 0) -> None:
+    """The DMA copies of the batched fused paths (csrc/utils.cpp:500-733):
+    staging tokens [offsets[i], + sizes[i]) <-> memory object i.
+    MLA/DSA objects: stacked planes, or per-token [K|V|DSA] rows when
+    token_major; MERGED/SEPARATE objects: [n, 2, W] (token_major, one range)
+    or [2, n, W] (K range, then V range at the object's stride 0)."""
+    mla = fmt in (MLA_KV, DSA_KV, MLA_LATENT, DSA_INDEX)
+    planes, _, _, pe = _layer_planes(caches, fmt, vllm_two_major, kH, vH, dsaH)
+    lmc_geo, N = _single_layer_lmc(staging, planes, pe, mla, token_major)
+    es = staging.es
+
+    def move(stg_off, obj, obj_off, nbytes):
+        if to_objects:
+            obj.data[obj_off: obj_off + nbytes] = staging.data[stg_off: stg_off + nbytes]
+        else:
+            staging.data[stg_off: stg_off + nbytes] = obj.data[obj_off: obj_off + nbytes]
+
+    for obj, off, n in zip(objs, offsets, sizes):
+        off, n = int(off), int(n)
+        assert off + n <= N
+        if mla:
+            for plane, (l0, lstride) in zip(planes, lmc_geo):
+                rb = plane[1]
+                for t in range(n):
+                    move(l0 + (off + t) * lstride, obj, _chunk_row_offset(plane, pe, n, t, es, token_major), rb)
+        elif token_major:
+            tok = lmc_geo[0][1]
+            move(off * tok, obj, 0, n * tok)
+        else:
+            tok = lmc_geo[0][1]
+            move(off * tok, obj, 0, n * tok)
+            move(lmc_geo[1][0] + off * tok, obj, obj.strides[0] * es, n * tok)
 
 
 def load_and_reshape_flash(kv: np.ndarray, num_layers: int, width: int, es: int,
