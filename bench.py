@@ -273,6 +273,81 @@ def bench_mla_576(torch, ops, dev, stream):
     return out
 
 
+def bench_direct(torch, ops, dev, stream):
+    """Sparse / direct single-layer transfers on one DeepSeek-style MLA layer
+    (kv_lora 512 + rope 64 bf16, 1024 blocks of 64 slots): dense direct store
+    and load of 16384 tokens in 64 pinned memory objects of 256 tokens
+    (PCIe); sparse direct retrieve of 2048 selected tokens from those
+    objects (PCIe); sparse single-layer scatter of 65536 selected tokens from
+    a device staging buffer (HBM); and the staged batched path on one
+    Llama-shape SEPARATE_KV layer (8 x 128, 4096 tokens in 16 pinned objects
+    of 256; PCIe)."""
+    NB, BS, KH, VH = 1024, 64, 512, 64
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn((NB, BS, 1, KH), device=dev, dtype=torch.bfloat16)
+    v = torch.randn((NB, BS, 1, VH), device=dev, dtype=torch.bfloat16)
+    caches = (k, v)
+    row = (KH + VH) * ES
+    T, CS = 16384, 256
+    slots = torch.randperm(NB * BS, generator=gen)[:T].to(dev)
+    objs = [torch.zeros(CS * (KH + VH), dtype=torch.bfloat16, pin_memory=True) for _ in range(T // CS)]
+    ptrs = ops._chunk_ptrs_for(objs, dev)
+    offs = torch.arange(0, T, CS, dtype=torch.int32, device=dev)
+    sizes = torch.full((T // CS,), CS, dtype=torch.int32, device=dev)
+    st = ops.prepare_sparse_direct_destination_state(caches, slots, 3, 0, 0, 0)
+    lay = ops.prepare_sparse_direct_layer_state(objs[0], caches, slots, False, False, 3, 0, 0, 0, CS)
+    store = lambda: ops.dense_mla_dsa_batched_direct_kv_transfer_fast(lay, slots, ptrs, offs, sizes, T, False, True,
+                                                                      False, CS)
+    load = lambda: ops.dense_mla_dsa_batched_direct_kv_transfer_prepared(st, slots, ptrs, offs, sizes, T, False,
+                                                                         False, CS)
+    NS = 2048
+    sel = torch.randperm(T, generator=gen)[:NS].to(torch.int32).to(dev)
+    sslots = torch.randperm(NB * BS, generator=gen)[:NS].to(dev)
+    sparse = lambda: ops.sparse_mla_dsa_batched_direct_kv_transfer_prepared(st, sslots, sel, ptrs, CS, T, False)
+    store(); load(); sparse()
+    t_st = time_events(torch, stream, store, 20)[0]
+    t_ld = time_events(torch, stream, load, 20)[0]
+    t_sp = time_events(torch, stream, sparse, 20)[0]
+    TH = 65536
+    staging = torch.randn(TH * (KH + VH), device=dev, dtype=torch.bfloat16)
+    hsel = torch.randperm(TH, generator=gen).to(torch.int32).to(dev)
+    hslots = torch.randperm(NB * BS, generator=gen)[:TH].to(dev)
+    scatter = lambda: ops.sparse_single_layer_kv_transfer(staging, caches, hslots, hsel, 3)
+    scatter()
+    t_sc = time_events(torch, stream, scatter, 20)[0]
+    # staged batched path, one Llama-shape layer
+    LT, LW = 4096, 8 * 128
+    lk = torch.randn((2048, 128, 8, 128), device=dev, dtype=torch.bfloat16)
+    lv = torch.randn((2048, 128, 8, 128), device=dev, dtype=torch.bfloat16)
+    lslots = torch.randperm(2048 * 128, generator=gen)[:LT].to(dev)
+    lobjs = [torch.zeros((2, 256, LW), dtype=torch.bfloat16, pin_memory=True) for _ in range(LT // 256)]
+    lstg = torch.empty((2, LT, LW), dtype=torch.bfloat16, device=dev)
+    loffs, lsizes = list(range(0, LT, 256)), [256] * (LT // 256)
+    bf_from = lambda: ops.batched_fused_single_layer_kv_transfer(lobjs, lstg, (lk, lv), lslots, loffs, lsizes, True, 2)
+    bf_to = lambda: ops.batched_fused_single_layer_kv_transfer(lobjs, lstg, (lk, lv), lslots, loffs, lsizes, False, 2)
+    bf_from(); bf_to()
+    t_bf = time_events(torch, stream, bf_from, 10)[0]
+    t_bt = time_events(torch, stream, bf_to, 10)[0]
+    torch.cuda.synchronize()
+
+    def pcie(nbytes, ms):
+        return {"ms": round(ms, 4), "payload_GBps": round(nbytes / ms / 1e6, 2),
+                "pcie_frac": round(nbytes / ms / 1e6 / PCIE_PEAK_GBS, 4)}
+
+    out = {
+        "direct_dense_store_mla_16k": pcie(T * row, t_st),
+        "direct_dense_load_mla_16k": pcie(T * row, t_ld),
+        "direct_sparse_load_mla_2048_of_16k": pcie(NS * row, t_sp),
+        "sparse_single_layer_mla_64k": {"ms": round(t_sc, 4), "payload_GBps": round(TH * row / t_sc / 1e6, 1),
+                                        "hbm_frac": round(2 * TH * row / t_sc / 1e6 / HBM_PEAK_GBS, 4)},
+        "batched_fused_from_gpu_llama_layer": pcie(2 * LT * LW * ES, t_bf),
+        "batched_fused_to_gpu_llama_layer": pcie(2 * LT * LW * ES, t_bt),
+    }
+    del k, v, objs, staging, lk, lv, lobjs, lstg
+    torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,7 +355,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576",
+    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -454,6 +529,8 @@ def main(argv=None):
         extra_big.update(bench_qwen32b_long_prefix(torch, ops, dev, stream))
     if "mla576" in sel:
         extra_big.update(bench_mla_576(torch, ops, dev, stream))
+    if "direct" in sel:
+        extra_big.update(bench_direct(torch, ops, dev, stream))
 
     def gbs(nbytes, ms):
         return round(nbytes / (ms * 1e-3) / 1e9, 2)

@@ -54,7 +54,10 @@ enum EntryMode : int32_t {
   kDenseVar = 1,
   kSparseChunked = 2,
   kSparseFlat = 3,
+  kDenseInline = 4,
 };
+
+constexpr int kInlineChunks = 64;  // chunk table entries carried in kernargs
 
 struct EntryJob {
   PlaneDesc plane[kMaxPlanes];
@@ -82,6 +85,18 @@ struct EntryJob {
   int64_t lmc_tokens;          // tokens the flat buffer holds
   int64_t n_entries;
   int32_t group_shift;         // log2 of lanes per entry
+  int32_t one_pass;            // every plane row fits one pass of the group
+  // kDenseInline: entry e is token tok_base + e of slot_mapping; chunk c
+  // covers tokens [inl_off[c], inl_off[c] + inl_size[c]) (ascending).
+  int64_t tok_base;
+  uint64_t inl_ptr[kInlineChunks];
+  int32_t inl_off[kInlineChunks];
+  int32_t inl_size[kInlineChunks];
+  // Optional second destination (dense modes): token g's row of plane p is
+  // also written at mirror + mirror_off[p] + g * mirror_stride[p].
+  uint64_t mirror;
+  int64_t mirror_off[kMaxPlanes];
+  int64_t mirror_stride[kMaxPlanes];
 };
 
 __device__ __forceinline__ int64_t load_index(const void *p, int is32,
@@ -90,36 +105,41 @@ __device__ __forceinline__ int64_t load_index(const void *p, int is32,
               : static_cast<const int64_t *>(p)[i];
 }
 
-// Resolves entry e to its slot, the token index t inside its chunk, the
-// chunk's token count and base; false when the entry is skipped.
+// Resolves entry e to its slot, its token g in slot_mapping (dense modes),
+// the token index t inside its chunk, the chunk's token count and base;
+// false when the entry's token lies in no chunk (the slot is checked by the
+// caller).
 __device__ __forceinline__ bool resolve(const EntryJob &job, int64_t e,
-                                        int64_t &slot, int64_t &t,
+                                        int64_t &slot, int64_t &g, int64_t &t,
                                         int64_t &nc, uint64_t &lbase) {
-  if (job.mode == kDenseFixed || job.mode == kDenseVar) {
-    slot = load_index(job.slots, job.slot_i32, e);
+  if (job.mode == kDenseFixed || job.mode == kDenseVar || job.mode == kDenseInline) {
+    g = job.tok_base + e;
+    slot = load_index(job.slots, job.slot_i32, g);
     int64_t c, start;
     if (job.mode == kDenseFixed) {
-      c = e / job.chunk_size;
+      c = g / job.chunk_size;
       start = c * job.chunk_size;
       nc = min(static_cast<int64_t>(job.chunk_size),
                static_cast<int64_t>(job.total_tokens) - start);
     } else {
-      // Last chunk whose offset is <= e.
-      if (job.chunk_offs[0] > e) return false;
+      // Last chunk whose offset is <= g.
+      const int32_t *offs = job.mode == kDenseInline ? job.inl_off : job.chunk_offs;
+      if (offs[0] > g) return false;
       int lo = 0, hi = job.n_chunks - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (job.chunk_offs[mid] <= e) lo = mid;
+        if (offs[mid] <= g) lo = mid;
         else hi = mid - 1;
       }
       c = lo;
-      start = job.chunk_offs[c];
-      nc = job.chunk_sizes[c];
+      start = offs[c];
+      nc = job.mode == kDenseInline ? job.inl_size[c] : job.chunk_sizes[c];
     }
-    if (c >= job.n_chunks || e >= start + nc) return false;
-    t = e - start;
-    lbase = static_cast<uint64_t>(job.chunk_ptrs[c]);
+    if (c >= job.n_chunks || g >= start + nc) return false;
+    t = g - start;
+    lbase = job.mode == kDenseInline ? job.inl_ptr[c] : static_cast<uint64_t>(job.chunk_ptrs[c]);
   } else {
+    g = e;
     if (job.counts != nullptr) {
       const int64_t r = e / job.row_width;
       if (r >= job.n_rows ||
@@ -143,7 +163,7 @@ __device__ __forceinline__ bool resolve(const EntryJob &job, int64_t e,
       lbase = job.lmc_flat;
     }
   }
-  return slot >= 0 && slot < job.num_slots;
+  return true;
 }
 
 template <int VEC, bool NT>
@@ -154,32 +174,79 @@ __global__ void __launch_bounds__(kEntThreads) kv_entry_copy(EntryJob job) {
   if (e >= job.n_entries) return;
   const int G = 1 << job.group_shift;
   const int gl = static_cast<int>(gid & (G - 1));
-  int64_t slot, t, nc;
+  int64_t slot, g, t, nc;
   uint64_t lbase;
-  if (!resolve(job, e, slot, t, nc, lbase)) return;
-  const bool aligned = (lbase & (VEC - 1)) == 0;
+  if (!resolve(job, e, slot, g, t, nc, lbase)) return;
+  // A skipped slot moves nothing, except with a mirror (the staging buffer
+  // of the batched paths): the memory object row and the staging row are
+  // then exchanged as the staged copies would (staging -> object when
+  // storing, object -> staging when loading).
+  const bool slot_ok = slot >= 0 && slot < job.num_slots;
+  if (!slot_ok && !job.mirror) return;
+  const bool third = job.mirror && slot_ok;
+  uint8_t *src[kMaxPlanes], *dst[kMaxPlanes], *mir[kMaxPlanes];
 #pragma unroll
   for (int p = 0; p < kMaxPlanes; ++p) {
-    if (p >= job.n_planes) break;
+    src[p] = dst[p] = mir[p] = nullptr;
+    if (p >= job.n_planes) continue;
     const PlaneDesc &pd = job.plane[p];
-    int64_t poff = pd.paged_off;
-    if (job.block_size > 0)
-      poff += (slot / job.block_size) * pd.blk_stride +
-              (slot % job.block_size) * pd.row_pitch;
-    else
-      poff += slot * pd.row_pitch;
-    uint8_t *paged = reinterpret_cast<uint8_t *>(job.base[p]) + poff;
     uint8_t *lm = reinterpret_cast<uint8_t *>(lbase) + pd.lmc_off_fixed +
                   pd.lmc_off_per_t * nc + t * pd.lmc_token_stride;
-    uint8_t *dst = job.page2lmc ? lm : paged;
-    const uint8_t *src = job.page2lmc ? paged : lm;
-    if (aligned) {
-      const int64_t nv = pd.row_bytes / VEC;
-      for (int64_t v = gl; v < nv; v += G)
-        st<V, NT>(reinterpret_cast<V *>(dst) + v,
-                  ld<V, NT>(reinterpret_cast<const V *>(src) + v));
+    uint8_t *m = job.mirror ? reinterpret_cast<uint8_t *>(job.mirror) + job.mirror_off[p] +
+                                  g * job.mirror_stride[p]
+                            : nullptr;
+    uint8_t *other;
+    if (slot_ok) {
+      int64_t poff = pd.paged_off;
+      if (job.block_size > 0)
+        poff += (slot / job.block_size) * pd.blk_stride +
+                (slot % job.block_size) * pd.row_pitch;
+      else
+        poff += slot * pd.row_pitch;
+      other = reinterpret_cast<uint8_t *>(job.base[p]) + poff;
+      mir[p] = m;
     } else {
-      for (int64_t b = gl; b < pd.row_bytes; b += G) dst[b] = src[b];
+      other = m;
+    }
+    dst[p] = job.page2lmc ? lm : other;
+    src[p] = job.page2lmc ? other : lm;
+  }
+  if ((lbase & (VEC - 1)) != 0) {  // unaligned chunk base: bytewise
+#pragma unroll
+    for (int p = 0; p < kMaxPlanes; ++p) {
+      if (p >= job.n_planes) continue;
+      for (int64_t b = gl; b < job.plane[p].row_bytes; b += G) {
+        const uint8_t x = src[p][b];
+        dst[p][b] = x;
+        if (third) mir[p][b] = x;
+      }
+    }
+    return;
+  }
+  if (job.one_pass) {
+    // Every plane's row fits one pass of the group: all loads, then all
+    // stores.
+    V x[kMaxPlanes];
+#pragma unroll
+    for (int p = 0; p < kMaxPlanes; ++p)
+      if (p < job.n_planes && gl * VEC < job.plane[p].row_bytes)
+        x[p] = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + gl);
+#pragma unroll
+    for (int p = 0; p < kMaxPlanes; ++p)
+      if (p < job.n_planes && gl * VEC < job.plane[p].row_bytes) {
+        st<V, NT>(reinterpret_cast<V *>(dst[p]) + gl, x[p]);
+        if (third) st<V, NT>(reinterpret_cast<V *>(mir[p]) + gl, x[p]);
+      }
+    return;
+  }
+#pragma unroll
+  for (int p = 0; p < kMaxPlanes; ++p) {
+    if (p >= job.n_planes) continue;
+    const int64_t nv = job.plane[p].row_bytes / VEC;
+    for (int64_t v = gl; v < nv; v += G) {
+      const V x = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + v);
+      st<V, NT>(reinterpret_cast<V *>(dst[p]) + v, x);
+      if (third) st<V, NT>(reinterpret_cast<V *>(mir[p]) + v, x);
     }
   }
 }
@@ -202,10 +269,12 @@ EntryJob entry_job(const LayerGeom &g, bool page2lmc) {
   return job;
 }
 
-// LMC side of host chunks of MLA/DSA formats: stacked planes
+// LMC side of memory objects laid out by plane: stacked planes
 // [K: n_c*kH | V: n_c*vH | DSA: n_c*dsaH] or per-token [K | V | DSA] rows
 // (csrc/utils.cpp:500-546; tools/cpu_vllm_runtime.py:299-338, 366-381).
-void chunk_layout_mla(const LayerGeom &g, bool interleaved, EntryJob &job) {
+// For MERGED/SEPARATE (planes K, V of width W) these are the [2, n, W] and
+// [n, 2, W] objects of the batched paths.
+void chunk_layout(const LayerGeom &g, bool interleaved, EntryJob &job) {
   for (int p = 0; p < g.n_planes; ++p) {
     PlaneDesc &d = job.plane[p];
     if (interleaved) {
@@ -233,11 +302,17 @@ void launch_entries(EntryJob job, bool host_lmc, hipStream_t stream) {
     widest = std::max(widest, d.row_bytes);
   }
   if (job.mode == kSparseFlat) gv = gcd64(gv, static_cast<int64_t>(job.lmc_flat & 0xff));
+  if (job.mirror) {
+    gv = gcd64(gv, static_cast<int64_t>(job.mirror & 0xff));
+    for (int p = 0; p < job.n_planes; ++p)
+      gv = gcd64(gcd64(gv, job.mirror_off[p]), job.mirror_stride[p]);
+  }
   const int vec = vec_for(gv);
   const int64_t vecs = std::max<int64_t>(1, widest / vec);
   int shift = 0;
   while ((int64_t(1) << shift) < vecs && shift < 6) ++shift;
   job.group_shift = shift;
+  job.one_pass = vecs <= (int64_t(1) << shift);
   const int64_t threads = job.n_entries << shift;
   const int64_t blocks = (threads + kEntThreads - 1) / kEntThreads;
   check(blocks < (int64_t(1) << 31), "too many entries in one call");
@@ -347,7 +422,7 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   EntryJob job = entry_job(g, false);
   job.mode = kSparseChunked;
   if (g.mla_dsa) {
-    chunk_layout_mla(g, interleaved, job);
+    chunk_layout(g, interleaved, job);
   } else {
     check(sample_t != nullptr,
           "MERGED/SEPARATE direct transfer needs an LMC layout sample");
@@ -438,7 +513,7 @@ void dense_direct(const lmc_tensor *ptrs_t, const lmc_tensor *caches, int n,
   DeviceGuard guard(g.device);
   EntryJob job = entry_job(g, page2lmc);
   job.mode = fixed > 0 ? kDenseFixed : kDenseVar;
-  chunk_layout_mla(g, interleaved, job);
+  chunk_layout(g, interleaved, job);
   job.slots = kernel_ptr(slots);
   job.slot_i32 = slots.dtype == LMC_I32;
   job.chunk_ptrs = reinterpret_cast<const int64_t *>(kernel_ptr(ptrs));
@@ -481,7 +556,10 @@ void copy_2d_async(void *dst, int64_t dpitch, const void *src, int64_t spitch,
 void stage_chunk(const LayerGeom &g, const PlaneDesc *sp, uint8_t *staging,
                  const lmc_tensor &obj, int64_t off, int64_t n,
                  bool token_major, bool to_host, hipStream_t s) {
-  uint8_t *host = kernel_ptr(obj);
+  // DMA copies take the object's own address (pinned or pageable host
+  // memory, or device memory).
+  uint8_t *host = static_cast<uint8_t *>(obj.data);
+  check(host != nullptr || obj.ndim == 0, "memory object has no storage");
   const int64_t es = g.es;
   check(elem_size(obj) == es, "memory object and cache dtypes differ");
   auto move = [&](uint8_t *stg, uint8_t *obj_p, int64_t bytes) {
@@ -534,6 +612,71 @@ void stage_chunks(const LayerGeom &g, const lmc_tensor &staging,
   }
 }
 
+// The batched path in one pass: when the memory objects are kernel-visible,
+// their chunks cover the staging tokens [0, T) in order and each object has
+// the layout the staged copies assume, every token's rows move between the
+// paged cache and its object by the entry kernel, which also writes them to
+// the staging buffer (the staging content the two-step path leaves, so the
+// results are the same bytes).  Returns false when the call does not
+// qualify; the caller then runs the two steps.
+bool batched_direct(const LayerGeom &g, const lmc_tensor &staging,
+                    const lmc_tensor *objs, int n_objs, const int64_t *offs,
+                    const int64_t *sizes, const lmc_tensor *slots_t,
+                    bool direction, bool token_major, hipStream_t stream) {
+  const lmc_tensor &slots = slots_of(slots_t);
+  const int64_t T = slots.sizes[0];
+  if (n_objs <= 0 || T <= 0 || T >= (int64_t(1) << 31) || staging.device < 0) return false;
+  PlaneDesc sp[kMaxPlanes];
+  std::memcpy(sp, g.plane, sizeof(sp));
+  if (elem_size(staging) != g.es || single_layer_lmc(g, staging, token_major, sp) < T) return false;
+  const int64_t W = g.width[0];
+  std::vector<uint64_t> ptrs(n_objs);
+  bool host = false;
+  for (int i = 0; i < n_objs; ++i) {
+    const int64_t n = sizes[i];
+    if (n <= 0 || offs[i] != (i == 0 ? 0 : offs[i - 1] + sizes[i - 1])) return false;
+    const lmc_tensor &o = objs[i];
+    if (elem_size(o) != g.es) return false;
+    int64_t need = n * g.plane_elems * g.es;
+    if (!g.mla_dsa && !token_major)
+      if (o.ndim < 2 || stride(o, 0) != n * W) return false;
+    if (extent_bytes(o) < need) return false;
+    if (o.device >= 0) {
+      ptrs[i] = reinterpret_cast<uint64_t>(o.data);
+    } else {
+      ptrs[i] = translate_host_ptr(reinterpret_cast<uintptr_t>(o.data),
+                                   static_cast<size_t>(need));
+      if (ptrs[i] == 0) return false;
+      host = true;
+    }
+  }
+  if (offs[n_objs - 1] + sizes[n_objs - 1] != T) return false;
+  EntryJob job = entry_job(g, direction);
+  job.mode = kDenseInline;
+  chunk_layout(g, token_major, job);
+  job.slots = kernel_ptr(slots);
+  job.slot_i32 = slots.dtype == LMC_I32;
+  job.mirror = reinterpret_cast<uint64_t>(kernel_ptr(staging));
+  for (int p = 0; p < g.n_planes; ++p) {
+    job.mirror_off[p] = sp[p].lmc_off_fixed;
+    job.mirror_stride[p] = sp[p].lmc_token_stride;
+  }
+  for (int c0 = 0; c0 < n_objs; c0 += kInlineChunks) {
+    const int nc = std::min(kInlineChunks, n_objs - c0);
+    EntryJob j = job;
+    j.n_chunks = nc;
+    for (int i = 0; i < nc; ++i) {
+      j.inl_ptr[i] = ptrs[c0 + i];
+      j.inl_off[i] = static_cast<int32_t>(offs[c0 + i]);
+      j.inl_size[i] = static_cast<int32_t>(sizes[c0 + i]);
+    }
+    j.tok_base = offs[c0];
+    j.n_entries = offs[c0 + nc - 1] + sizes[c0 + nc - 1] - offs[c0];
+    launch_entries(j, host, stream);
+  }
+  return true;
+}
+
 void batched_fused(const lmc_tensor *objs, int n_objs, const lmc_tensor *staging_t,
                    const lmc_tensor *caches, int n, const lmc_tensor *slots_t,
                    const int64_t *offs, const int64_t *sizes, bool direction,
@@ -543,6 +686,9 @@ void batched_fused(const lmc_tensor *objs, int n_objs, const lmc_tensor *staging
   const lmc_tensor &staging = deref(staging_t, "staging_cache");
   check(n_objs >= 0 && (n_objs == 0 || (objs && offs && sizes)), "bad chunk list");
   DeviceGuard guard(g.device);
+  if (batched_direct(g, staging, objs, n_objs, offs, sizes, slots_t, direction,
+                     token_major, stream))
+    return;
   if (direction) {
     single_layer(staging_t, caches, n, slots_t, true, fmt, token_major, two_major,
                  kH, vH, dsaH, stream);

@@ -169,19 +169,29 @@ def _obj_shape(fmt, n, pe, token_major):
 @pytest.mark.parametrize("fmt,two_major", [(1, False), (1, True), (2, False), (3, False), (4, False)])
 @pytest.mark.parametrize("token_major", [False, True])
 @pytest.mark.parametrize("num_chunks", [1, 3, 5])
-def test_batched_fused_single_layer(ops, fmt, two_major, token_major, num_chunks):
-    """tests/v1/test_mem_kernels.py:791-1062: equal to one single-layer copy
-    through the staging buffer plus per-chunk copies, both directions."""
+@pytest.mark.parametrize("objects", ["pinned", "pageable", "gap"])
+def test_batched_fused_single_layer(ops, fmt, two_major, token_major, num_chunks, objects):
+    """tests/v1/test_mem_kernels.py:791-1062: equal, byte for byte (memory
+    objects, paged caches and the staging buffer), to one single-layer copy
+    through the staging buffer plus per-chunk copies, both directions, with
+    some slots -1.  Pinned objects covering the staging tokens take the
+    one-pass kernel; pageable objects and a chunk list with a gap take the
+    two-step path."""
     T = 256
     g = torch.Generator().manual_seed(100 * fmt + 10 * num_chunks + token_major)
     src = paged_caches(fmt, g, two_major=two_major)
     dst = paged_caches(fmt, g, two_major=two_major)
     pe = plane_elems(fmt, src)
-    slots = torch.randperm(32 * 16, generator=g)[:T].to(DEV)
+    slots = torch.randperm(32 * 16, generator=g)[:T]
+    slots[[5, 130]] = -1
+    slots = slots.to(DEV)
     offs, sizes = _chunks_of(T, num_chunks)
+    if objects == "gap":
+        sizes[-1] -= 3
     stg_shape = _obj_shape(fmt, T, pe, token_major)
-    staging = torch.zeros(stg_shape, dtype=torch.bfloat16, device=DEV)
-    objs = [torch.zeros(_obj_shape(fmt, n, pe, token_major), dtype=torch.bfloat16, pin_memory=True) for n in sizes]
+    staging = randn_bf16(stg_shape, g).to(DEV)
+    pin = objects != "pageable"
+    objs = [torch.zeros(_obj_shape(fmt, n, pe, token_major), dtype=torch.bfloat16, pin_memory=pin) for n in sizes]
     # from_gpu
     want_stg = tb(staging)
     want_objs = [tb(o) for o in objs]
@@ -193,19 +203,25 @@ def test_batched_fused_single_layer(ops, fmt, two_major, token_major, num_chunks
     torch.cuda.synchronize()
     for o, w in zip(objs, want_objs):
         assert same(o, w)
-    # to_gpu
+    assert same(staging, want_stg)
+    # to_gpu (objects perturbed first so staging rows change)
+    for o in objs:
+        o.add_(1.0)
+    want_objs = [tb(o) for o in objs]
     want_dst = [tb(c) for c in dst]
-    stg2 = ok.TensorBytes(np.zeros_like(want_stg.data), want_stg.shape, want_stg.strides, 2)
-    ok.stage_chunks(stg2, [tb(c) for c in dst], want_objs, offs, sizes, fmt, token_major, False, two_major)
-    ok.single_layer_kv_transfer(stg2, want_dst, slots.cpu().numpy(), False, fmt, token_major, two_major)
+    ok.stage_chunks(want_stg, [tb(c) for c in dst], want_objs, offs, sizes, fmt, token_major, False, two_major)
+    ok.single_layer_kv_transfer(want_stg, want_dst, slots.cpu().numpy(), False, fmt, token_major, two_major)
     ops.batched_fused_single_layer_kv_transfer(objs, staging, arg_caches(dst), slots, offs, sizes, False, fmt,
                                                token_major, two_major)
     torch.cuda.synchronize()
     for c, w in zip(dst, want_dst):
         assert same(c, w)
-    # the reference test's own check: dst rows now equal src rows
-    if fmt in (ok.MERGED_KV, ok.SEPARATE_KV):
+    assert same(staging, want_stg)
+    # the reference test's own check: dst rows now equal src rows + 1
+    if fmt in (ok.MERGED_KV, ok.SEPARATE_KV) and objects != "gap":
+        slots = slots[slots >= 0]
         for a, b in zip(src, dst):
+            a = a + 1.0
             if fmt == ok.MERGED_KV:
                 for p in range(2):
                     ap = a[p] if two_major else a[:, p]
