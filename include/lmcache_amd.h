@@ -241,6 +241,47 @@ int lmc_batched_fused_sparse_single_layer_kv_transfer(
     int64_t k_hidden_dims, int64_t v_hidden_dims, int64_t dsa_hidden_dims,
     void *stream);
 
+/* Replaces sparse_graph_kv_transfer and its sfa_copy kernels
+ * (csrc/mem_kernels.cpp:742-831; csrc/graph/sparse_graph_kernel.cpp:6-132;
+ * pybind csrc/pybind.cpp:437-440): entry (r, j) of the packed
+ * [requests, row_width] `selected` / `slots` matrices, active for j <
+ * min(counts[r * stride(0)], row_width) when counts and limits[r] are > 0,
+ * copies token selected[r, j] in [0, limits[r]) from the chunk sources
+ * ptrs[0 | 1, r * chunks_per_request + token / chunk_size] (K, PE; null
+ * skips) into row slots[r, j] of k_cache / pe_cache.  k_hidden_dims /
+ * pe_hidden_dims <= 0 take the caches' last two dims.  max_aiv_cores is
+ * accepted and does not change the result. */
+int lmc_sparse_graph_kv_transfer(const lmc_tensor *k_cache, const lmc_tensor *pe_cache,
+                                 int64_t k_hidden_dims, int64_t pe_hidden_dims,
+                                 const lmc_tensor *slots, const lmc_tensor *selected,
+                                 const lmc_tensor *counts, const lmc_tensor *ptrs,
+                                 const lmc_tensor *limits, int64_t chunk_size,
+                                 int64_t max_aiv_cores, void *stream);
+
+/* IndexerC8State's checks (csrc/indexer_c8.cpp:13-50): keys
+ * [NB, 128, 1, 128] float16/bfloat16 alone, or int8 with float16 scales
+ * [NB, 128, 1, 1]; slot_factor 1 (or 2 for int8); optional int32 block_map
+ * [NB] (int8, factor 1).  scales and block_map may be NULL. */
+int lmc_indexer_c8_check_state(const lmc_tensor *keys, const lmc_tensor *scales,
+                               int64_t slot_factor, const lmc_tensor *block_map);
+
+/* Replaces indexer_c8_transfer_prepared and indexer_c8_group_transfer_prepared
+ * (csrc/indexer_c8.cpp:52-185; csrc/indexer_c8/kernel.cpp:29-121; pybind
+ * csrc/pybind.cpp:243-262): for each of n_layers layers (per-layer keys,
+ * scales, block_maps entries may be NULL, slot_factors[l]) and each chunk c
+ * (packet packet_ptrs[l, c]; tokens [start, start + count) of slot_mapping,
+ * start / count from chunk_offsets / chunk_counts or, with fixed_chunks, c *
+ * chunk_capacity and the rest of the mapping), token t's key row and scale
+ * move between the packet ([count key rows | count scales]) and the cache's
+ * physical slot (block_map[s / 128] * 128 + s % 128, or s + (s / 128) *
+ * (slot_factor - 1) * 128).  from_npu != 0: cache -> packet. */
+int lmc_indexer_c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
+                            const lmc_tensor *const *block_maps, const int64_t *slot_factors,
+                            int32_t n_layers, const lmc_tensor *packet_ptrs,
+                            const lmc_tensor *chunk_offsets, const lmc_tensor *chunk_counts,
+                            const lmc_tensor *slot_mapping, int64_t chunk_capacity,
+                            int32_t from_npu, int32_t fixed_chunks, void *stream);
+
 /* The cache checks of prepare_sparse_direct_layer_state /
  * prepare_sparse_direct_destination_state (csrc/utils.cpp:408-498,
  * 903-966): LMC_ERR_VALUE with the reference's message on a bad format or

@@ -1,0 +1,260 @@
+// Indexer key / C8 packet transport for MI355X (gfx950).
+//
+// Replaces indexer_c8_transfer_prepared / indexer_c8_group_transfer_prepared
+// and their state checks (csrc/indexer_c8.cpp:12-185; device semantics
+// csrc/indexer_c8/kernel.cpp:29-121).  A layer's destination is a paged
+// indexer cache: keys [NB, 128, 1, 128] (float16 / bfloat16, 256 bytes per
+// slot; or int8, 128 bytes per slot, with float16 scales [NB, 128, 1, 1]).
+// A packet holds one chunk of tokens: `count` key rows, then, for int8
+// keys, `count` 2-byte scales.  Token t of chunk c is slot_mapping[start_c +
+// t]; its physical cache slot is
+//
+//   block_map[slot / 128] * 128 + slot % 128            (block permutation)
+//   slot + (slot / 128) * (slot_factor - 1) * 128       (otherwise)
+//
+// and its key row and scale move between packet and cache (from_npu: cache
+// -> packet).  Chunks with a null packet or an impossible range, slots
+// outside [0, cache_slots) and physical slots outside the cache are
+// skipped, as in the reference kernel.
+//
+// Work mapping: grid (token tiles of the chunk capacity, chunk, layer); a
+// group of 16 lanes owns a token: up to 16 lanes move its key row in
+// 16-byte accesses (bytewise when the packet is not 16-byte aligned) and
+// one lane its scale.  Every access is bounded by the checks above.
+#include "common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+namespace lmc {
+
+namespace {
+
+constexpr int kC8Threads = 256;
+constexpr int kC8Group = 16;             // lanes per token
+constexpr int kC8Layers = 32;            // layers per launch (kernargs)
+constexpr int kC8Tokens = kC8Threads / kC8Group;
+
+struct C8Layer {
+  uint64_t keys;
+  uint64_t scales;     // 0: floating keys without scales
+  uint64_t block_map;  // 0: no block permutation
+  int32_t key_bytes;
+  int32_t slot_factor;
+};
+
+struct C8Job {
+  C8Layer layer[kC8Layers];
+  const int64_t *packets;   // [layers, chunks] (rows of this launch)
+  const void *offsets;
+  const void *counts;
+  const void *slots;
+  int32_t meta_i32;
+  int32_t slot_i32;
+  int32_t from_npu;
+  int32_t fixed;
+  int64_t chunks;
+  int64_t capacity;
+  int64_t slot_count;
+  int64_t cache_slots;
+};
+
+__device__ __forceinline__ int64_t c8_index(const void *p, int is32, int64_t i) {
+  return is32 ? static_cast<int64_t>(static_cast<const int32_t *>(p)[i])
+              : static_cast<const int64_t *>(p)[i];
+}
+
+__global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
+  const int64_t c = blockIdx.y;
+  const int li = blockIdx.z;
+  const C8Layer &L = job.layer[li];
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kC8Tokens + threadIdx.x / kC8Group;
+  const int gl = threadIdx.x % kC8Group;
+  const int64_t start = job.fixed ? c * job.capacity : c8_index(job.offsets, job.meta_i32, c);
+  const int64_t remaining = job.slot_count - start;
+  const int64_t count = job.fixed ? (remaining < job.capacity ? remaining : job.capacity)
+                                  : c8_index(job.counts, job.meta_i32, c);
+  const uint64_t packet = static_cast<uint64_t>(job.packets[li * job.chunks + c]);
+  if (!packet || count <= 0 || count > job.capacity || start < 0 ||
+      start > job.slot_count || count > job.slot_count - start || t >= count)
+    return;
+  const int64_t slot = c8_index(job.slots, job.slot_i32, start + t);
+  if (slot < 0 || slot >= job.cache_slots) return;
+  const int64_t phys =
+      L.block_map
+          ? static_cast<int64_t>(reinterpret_cast<const int32_t *>(L.block_map)[slot / 128]) * 128 +
+                slot % 128
+          : slot + (slot / 128) * (L.slot_factor - 1) * 128;
+  if (phys < 0 || phys + 1 > job.cache_slots * L.slot_factor) return;
+  uint8_t *pk = reinterpret_cast<uint8_t *>(packet) + t * L.key_bytes;
+  uint8_t *ck = reinterpret_cast<uint8_t *>(L.keys) + phys * L.key_bytes;
+  uint8_t *dst = job.from_npu ? pk : ck;
+  const uint8_t *src = job.from_npu ? ck : pk;
+  if ((packet & 15) == 0) {
+    using V = unsigned int __attribute__((ext_vector_type(4)));
+    for (int v = gl; v < L.key_bytes / 16; v += kC8Group)
+      reinterpret_cast<V *>(dst)[v] = reinterpret_cast<const V *>(src)[v];
+  } else {
+    for (int b = gl; b < L.key_bytes; b += kC8Group) dst[b] = src[b];
+  }
+  if (L.scales && gl == 0) {
+    uint8_t *ps = reinterpret_cast<uint8_t *>(packet) + count * L.key_bytes + t * 2;
+    uint8_t *cs = reinterpret_cast<uint8_t *>(L.scales) + phys * 2;
+    uint8_t *d = job.from_npu ? ps : cs;
+    const uint8_t *s = job.from_npu ? cs : ps;
+    d[0] = s[0];
+    d[1] = s[1];
+  }
+}
+
+// IndexerC8State's checks (csrc/indexer_c8.cpp:13-50), with its messages.
+void check_state(const lmc_tensor &keys, const lmc_tensor *scales,
+                 int64_t factor, const lmc_tensor *block_map) {
+  check(keys.device >= 0 && (scales == nullptr || scales->device == keys.device),
+        "C8 destinations must share one GPU device");
+  const bool quantized = keys.dtype == LMC_I8;
+  check(quantized ? scales != nullptr && scales->dtype == LMC_F16
+                  : scales == nullptr && (keys.dtype == LMC_F16 || keys.dtype == LMC_BF16),
+        "Indexer requires floating keys alone, or int8 keys and float16 scales");
+  auto contiguous = [](const lmc_tensor &t) {
+    int64_t expect = 1;
+    for (int i = t.ndim - 1; i >= 0; --i) {
+      if (t.sizes[i] != 1 && t.strides[i] != expect) return false;
+      expect *= t.sizes[i];
+    }
+    return true;
+  };
+  check(keys.ndim == 4 && keys.sizes[0] > 0 && keys.sizes[1] == 128 && keys.sizes[2] == 1 &&
+            keys.sizes[3] == 128 && contiguous(keys),
+        "Indexer destinations require contiguous PA_BSND storage");
+  check((factor == 1 || (factor == 2 && quantized)) && keys.sizes[0] % factor == 0,
+        "Invalid physical indexer block factor");
+  check(!quantized || (scales->ndim == 4 && scales->sizes[0] == keys.sizes[0] &&
+                       scales->sizes[1] == 128 && scales->sizes[2] == 1 &&
+                       scales->sizes[3] == 1 && contiguous(*scales)),
+        "C8 destinations require paired contiguous PA_BSND storage");
+  check(block_map == nullptr ||
+            (quantized && factor == 1 && block_map->device == keys.device &&
+             block_map->dtype == LMC_I32 && block_map->ndim == 1 &&
+             block_map->sizes[0] == keys.sizes[0] && contiguous(*block_map)),
+        "C8 block permutation must be a complete contiguous int32 vector on the "
+        "cache device");
+}
+
+int64_t cache_slots_of(const lmc_tensor &keys, int64_t factor) {
+  return numel(keys) / 128 / factor;
+}
+
+void check_vector(const lmc_tensor &t, int device) {
+  check(t.device == device && (t.dtype == LMC_I64 || t.dtype == LMC_I32) && t.ndim == 1 &&
+            (t.sizes[0] <= 1 || t.strides[0] == 1),
+        "C8 copy metadata must be contiguous int32/int64 vectors on the cache device");
+}
+
+void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
+                 const lmc_tensor *const *maps, const int64_t *factors, int n_layers,
+                 const lmc_tensor &ptrs, const lmc_tensor &offs, const lmc_tensor &counts,
+                 const lmc_tensor &slots, int64_t capacity, bool from_npu, bool fixed,
+                 hipStream_t stream) {
+  check(n_layers > 0 && keys && factors, "C8 group must contain at least one layer");
+  C8Job job;
+  std::memset(&job, 0, sizeof(job));
+  const lmc_tensor &k0 = deref(keys[0], "keys");
+  const int dev = k0.device;
+  int64_t cache_slots = -1;
+  for (int l = 0; l < n_layers; ++l) {
+    const lmc_tensor &k = deref(keys[l], "keys");
+    const lmc_tensor *s = scales ? scales[l] : nullptr;
+    const lmc_tensor *m = maps ? maps[l] : nullptr;
+    check_state(k, s, factors[l], m);
+    const int64_t cs = cache_slots_of(k, factors[l]);
+    check(k.device == dev && (cache_slots < 0 || cs == cache_slots),
+          "C8 group layers must share device and slot capacity");
+    cache_slots = cs;
+  }
+  // csrc/indexer_c8.cpp:65-95 (a group's pointers are [layers, chunks]).
+  if (n_layers > 1 || ptrs.ndim == 2) {
+    check(ptrs.ndim == 2 && ptrs.sizes[0] == n_layers &&
+              (ptrs.sizes[1] <= 1 || (ptrs.strides[1] == 1 && ptrs.strides[0] == ptrs.sizes[1])),
+          "C8 group pointers must have shape [layers, chunks]");
+    check(ptrs.device == dev && ptrs.dtype == LMC_I64,
+          "C8 copy metadata must be contiguous int32/int64 vectors on the cache device");
+  } else {
+    check_vector(ptrs, dev);
+  }
+  check_vector(offs, dev);
+  check_vector(counts, dev);
+  check_vector(slots, dev);
+  check(ptrs.dtype == LMC_I64 && offs.dtype == counts.dtype,
+        "C8 pointers must be int64; offsets and counts must share a dtype");
+  const int64_t chunks = ptrs.ndim == 2 ? ptrs.sizes[1] : ptrs.sizes[0];
+  check(fixed || (numel(offs) == chunks && numel(counts) == chunks),
+        "C8 pointer, offset and count vectors must have equal lengths");
+  check(capacity > 0 && capacity <= INT32_MAX, "C8 chunk capacity is out of range");
+  if (chunks == 0) return;
+  const int64_t slot_count = numel(slots);
+  check(!fixed || (slot_count + capacity - 1) / capacity == chunks,
+        "C8 fixed chunks do not cover the slot mapping");
+  check(chunks <= 65535, "C8 transfer has more chunks than one launch grid holds");
+  DeviceGuard guard(dev);
+  job.offsets = offs.data;
+  job.counts = counts.data;
+  job.slots = slots.data;
+  job.meta_i32 = offs.dtype == LMC_I32;
+  job.slot_i32 = slots.dtype == LMC_I32;
+  job.from_npu = from_npu ? 1 : 0;
+  job.fixed = fixed ? 1 : 0;
+  job.chunks = chunks;
+  job.capacity = capacity;
+  job.slot_count = slot_count;
+  job.cache_slots = cache_slots;
+  const int64_t tiles = (capacity + kC8Tokens - 1) / kC8Tokens;
+  check(tiles < (int64_t(1) << 31), "C8 transfer grid is too large");
+  for (int l0 = 0; l0 < n_layers; l0 += kC8Layers) {
+    const int nl = std::min(kC8Layers, n_layers - l0);
+    C8Job j = job;
+    j.packets = static_cast<const int64_t *>(ptrs.data) + static_cast<int64_t>(l0) * chunks;
+    for (int i = 0; i < nl; ++i) {
+      const lmc_tensor &k = *keys[l0 + i];
+      C8Layer &L = j.layer[i];
+      L.keys = reinterpret_cast<uint64_t>(k.data);
+      L.scales = scales && scales[l0 + i] ? reinterpret_cast<uint64_t>(scales[l0 + i]->data) : 0;
+      L.block_map = maps && maps[l0 + i] ? reinterpret_cast<uint64_t>(maps[l0 + i]->data) : 0;
+      L.key_bytes = static_cast<int32_t>(128 * elem_size(k));
+      L.slot_factor = static_cast<int32_t>(factors[l0 + i]);
+    }
+    hipLaunchKernelGGL(indexer_c8_copy, dim3(static_cast<unsigned>(tiles), chunks, nl),
+                       dim3(kC8Threads), 0, stream, j);
+    hip_check(hipGetLastError(), "indexer_c8_copy launch");
+  }
+}
+
+} // namespace
+} // namespace lmc
+
+using namespace lmc;
+
+extern "C" {
+
+int lmc_indexer_c8_check_state(const lmc_tensor *keys, const lmc_tensor *scales,
+                               int64_t slot_factor, const lmc_tensor *block_map) {
+  return guarded([&] { check_state(deref(keys, "keys"), scales, slot_factor, block_map); });
+}
+
+int lmc_indexer_c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
+                            const lmc_tensor *const *block_maps, const int64_t *slot_factors,
+                            int32_t n_layers, const lmc_tensor *packet_ptrs,
+                            const lmc_tensor *chunk_offsets, const lmc_tensor *chunk_counts,
+                            const lmc_tensor *slot_mapping, int64_t chunk_capacity,
+                            int32_t from_npu, int32_t fixed_chunks, void *stream) {
+  return guarded([&] {
+    c8_transfer(keys, scales, block_maps, slot_factors, n_layers,
+                deref(packet_ptrs, "packet_ptrs"), deref(chunk_offsets, "chunk_offsets"),
+                deref(chunk_counts, "chunk_counts"), deref(slot_mapping, "slot_mapping"),
+                chunk_capacity, from_npu != 0, fixed_chunks != 0,
+                static_cast<hipStream_t>(stream));
+  });
+}
+
+} // extern "C"

@@ -76,6 +76,12 @@ SIGNATURES = {
         _i64, _i64, _i64, _vp,
     ],
     "lmc_check_kv_caches": [_T, _i32, _i32, _i32, _i64, _i64, _i64],
+    "lmc_sparse_graph_kv_transfer": [_T, _T, _i64, _i64, _T, _T, _T, _T, _T, _i64, _i64, _vp],
+    "lmc_indexer_c8_check_state": [_T, _T, _i64, _T],
+    "lmc_indexer_c8_transfer": [
+        ctypes.POINTER(_T), ctypes.POINTER(_T), ctypes.POINTER(_T), ctypes.POINTER(_i64), _i32, _T, _T, _T, _T,
+        _i64, _i32, _i32, _vp,
+    ],
     "lmc_calculate_cdf": [_T, _i32, _T, _vp],
     "lmc_encode_fast_new": [_T, _T, _T, _T, _vp],
     "lmc_decode_fast_new": [_T, _T, _T, _T, _vp],

@@ -771,6 +771,97 @@ def dense_mla_dsa_group_direct_kv_transfer_prepared(
                  fixed_chunk_size)
 
 
+def sparse_graph_kv_transfer(destination_state, slots, selected, counts, ptrs, limits, chunk_size,
+                             max_aiv_cores=0) -> None:
+    """Graph-replay sparse copy into a prepared MLA destination
+    (csrc/mem_kernels.cpp:742-831; csrc/graph/sparse_graph_kernel.cpp):
+    rows of `selected` / `slots` per request, `counts` and `limits` per row,
+    `ptrs` the [2, requests * chunks] K and PE chunk-source tables."""
+    st = destination_state
+    k, pe = st.caches[0], st.caches[1]
+    a, b = _desc(k), _desc(pe)
+    d = [_desc(x) for x in (slots, selected, counts, ptrs, limits)]
+    dev = _device_index(selected, k)
+    _run(
+        _L.lmc_sparse_graph_kv_transfer(
+            _ref(a), _ref(b), int(st.k_hidden_dims), int(st.v_hidden_dims), *[_ref(x) for x in d],
+            int(chunk_size), int(max_aiv_cores), _stream(dev),
+        )
+    )
+
+
+# ---------------------------------------------------------------------------
+# Indexer key / C8 packet transport (csrc/indexer_c8.cpp; pybind.cpp:243-262)
+# ---------------------------------------------------------------------------
+
+INDEXER_C8_BLOCK_MAP_ABI = 1
+
+
+class IndexerC8State:
+    """One layer's indexer cache: float16/bfloat16 keys [NB, 128, 1, 128],
+    or int8 keys with float16 scales [NB, 128, 1, 1]; physical slot factor
+    1 (or 2 for int8) or an int32 block permutation (csrc/indexer_c8.cpp:
+    13-50)."""
+
+    def __init__(self, keys, scales=None, slot_factor=1, block_map=None):
+        kd = _desc(keys)
+        sd = _desc(scales) if scales is not None else None
+        md = _desc(block_map) if block_map is not None else None
+        _run(_L.lmc_indexer_c8_check_state(_ref(kd), _ref(sd) if sd is not None else None, int(slot_factor),
+                                           _ref(md) if md is not None else None))
+        self.keys, self.scales, self.block_map = keys, scales, block_map
+        self.slot_factor = int(slot_factor)
+        self.cache_slots = keys.numel() // 128 // self.slot_factor
+        self.key_bytes = 128 * keys.element_size()
+
+
+class IndexerC8GroupState:
+    """Several layers moved by one launch (csrc/indexer_c8.cpp:52-74)."""
+
+    def __init__(self, layers):
+        layers = list(layers)
+        if not layers:
+            raise RuntimeError("C8 group must contain at least one layer")
+        for st in layers:
+            if st.keys.device != layers[0].keys.device or st.cache_slots != layers[0].cache_slots:
+                raise RuntimeError("C8 group layers must share device and slot capacity")
+        self.layers = layers
+        self.max_key_bytes = max([128] + [st.key_bytes for st in layers])
+
+
+def _c8(layers, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu, fixed_chunks):
+    n = len(layers)
+    keys = [_desc(st.keys) for st in layers]
+    scales = [_desc(st.scales) if st.scales is not None else None for st in layers]
+    maps = [_desc(st.block_map) if st.block_map is not None else None for st in layers]
+    P = ctypes.POINTER(_lib.LmcTensor)
+    ka = (P * n)(*[ctypes.pointer(x) for x in keys])
+    sa = (P * n)(*[ctypes.pointer(x) if x is not None else P() for x in scales])
+    ma = (P * n)(*[ctypes.pointer(x) if x is not None else P() for x in maps])
+    fa = (ctypes.c_int64 * n)(*[st.slot_factor for st in layers])
+    d = [_desc(x) for x in (packet_ptrs, chunk_offsets, chunk_counts, slot_mapping)]
+    dev = _device_index(layers[0].keys)
+    _run(
+        _L.lmc_indexer_c8_transfer(
+            ka, sa, ma, fa, n, *[_ref(x) for x in d], int(chunk_capacity), int(bool(from_npu)),
+            int(bool(fixed_chunks)), _stream(dev),
+        )
+    )
+
+
+def indexer_c8_transfer_prepared(state, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity,
+                                 from_npu, fixed_chunks=False) -> None:
+    """csrc/indexer_c8.cpp:139-158."""
+    _c8([state], packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu, fixed_chunks)
+
+
+def indexer_c8_group_transfer_prepared(state, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping,
+                                       chunk_capacity, from_npu, fixed_chunks=False) -> None:
+    """csrc/indexer_c8.cpp:160-184: packet_ptrs is [layers, chunks]."""
+    _c8(state.layers, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu,
+        fixed_chunks)
+
+
 # ---------------------------------------------------------------------------
 # Pinned host memory
 # ---------------------------------------------------------------------------

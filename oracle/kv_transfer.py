@@ -402,3 +402,80 @@ def fused_required_size(fmt: int, use_mla: bool, L: int, T: int, W: int, kH: int
     if fmt == DSA_INDEX:
         return L * T * dsaH * es
     return (1 if use_mla else 2) * L * T * W * es
+
+
+def sparse_graph_kv_transfer(k_rows: np.ndarray, pe_rows: np.ndarray, k_bytes: int, pe_bytes: int,
+                             slots: np.ndarray, selected: np.ndarray, row_counts, limits,
+                             k_sources: Sequence, pe_sources: Sequence, chunk_size: int) -> None:
+    """sparse_graph_kv_transfer (csrc/graph/sparse_graph_kernel.cpp:6-72):
+    k_rows / pe_rows are the destination caches' bytes (flat rows);
+    selected / slots are [requests, row_width]; row_counts[r] is the row's
+    count (counts[r * stride]); k_sources / pe_sources list, per request and
+    chunk (index r * chunks_per_request + chunk), a byte array or None."""
+    R, width = selected.shape
+    cpr = len(k_sources) // R
+    dest_slots = min(k_rows.size // k_bytes, pe_rows.size // pe_bytes)
+    for r in range(R):
+        lim, cnt = int(limits[r]), int(row_counts[r])
+        active = 0 if lim <= 0 or cnt <= 0 else min(cnt, width)
+        for j in range(active):
+            tok, dst = int(selected[r, j]), int(slots[r, j])
+            if tok < 0 or tok >= lim or dst < 0 or dst >= dest_slots:
+                continue
+            chunk, off = divmod(tok, chunk_size)
+            if chunk >= cpr:
+                continue
+            ks, ps = k_sources[r * cpr + chunk], pe_sources[r * cpr + chunk]
+            if ks is None or ps is None:
+                continue
+            k_rows[dst * k_bytes:(dst + 1) * k_bytes] = ks[off * k_bytes:(off + 1) * k_bytes]
+            pe_rows[dst * pe_bytes:(dst + 1) * pe_bytes] = ps[off * pe_bytes:(off + 1) * pe_bytes]
+
+
+@dataclass
+class C8Layer:
+    """One indexer layer: key rows (key_bytes per physical slot), optional
+    2-byte scales, slot factor, optional int32 block map, logical slots."""
+    keys: np.ndarray
+    scales: np.ndarray
+    key_bytes: int
+    slot_factor: int
+    block_map: np.ndarray
+    cache_slots: int
+
+
+def indexer_c8_transfer(layers: Sequence[C8Layer], packets: Sequence[Sequence], offsets, counts,
+                        slots: np.ndarray, capacity: int, from_npu: bool, fixed: bool) -> None:
+    """indexer_c8_transfer_prepared / _group_ (csrc/indexer_c8/kernel.cpp:
+    29-121): packets[l][c] is chunk c's packet of layer l (bytes, or None):
+    `count` key rows then `count` 2-byte scales."""
+    slot_count = slots.shape[0]
+    for l, L in enumerate(layers):
+        for c, packet in enumerate(packets[l]):
+            start = c * capacity if fixed else int(offsets[c])
+            count = min(slot_count - start, capacity) if fixed else int(counts[c])
+            if (packet is None or count <= 0 or count > capacity or start < 0 or start > slot_count
+                    or count > slot_count - start):
+                continue
+            for t in range(count):
+                s = int(slots[start + t])
+                if s < 0 or s >= L.cache_slots:
+                    continue
+                if L.block_map is not None:
+                    phys = int(L.block_map[s // 128]) * 128 + s % 128
+                else:
+                    phys = s + (s // 128) * (L.slot_factor - 1) * 128
+                if phys < 0 or phys + 1 > L.cache_slots * L.slot_factor:
+                    continue
+                kb = L.key_bytes
+                pk, ck = slice(t * kb, (t + 1) * kb), slice(phys * kb, (phys + 1) * kb)
+                if from_npu:
+                    packet[pk] = L.keys[ck]
+                else:
+                    L.keys[ck] = packet[pk]
+                if L.scales is not None:
+                    ps, cs = slice(count * kb + 2 * t, count * kb + 2 * t + 2), slice(2 * phys, 2 * phys + 2)
+                    if from_npu:
+                        packet[ps] = L.scales[cs]
+                    else:
+                        L.scales[cs] = packet[ps]
