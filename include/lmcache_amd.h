@@ -364,6 +364,46 @@ int lmc_alloc_pinned_ptr(size_t size, uint32_t flags, uintptr_t *out_ptr);
  * csrc/pybind.cpp:348). */
 int lmc_free_pinned_ptr(uintptr_t ptr);
 
+/* Replaces alloc_pinned_numa_ptr (csrc/common/mem_alloc.cpp:56-92; pybind
+ * csrc/pybind.cpp:349-350): zeroed page-locked host memory placed on NUMA
+ * node `node` (the calling thread's policy is bound to it for the
+ * allocation and restored afterwards), mapped into the device address space
+ * and recorded for lmc_get_device_ptr. */
+int lmc_alloc_pinned_numa_ptr(size_t size, int32_t node, uintptr_t *out_ptr);
+
+/* Replaces free_pinned_numa_ptr (csrc/common/mem_alloc.cpp:94-106; pybind
+ * csrc/pybind.cpp:351).  `size` is accepted for the reference's
+ * signature; the runtime knows the allocation's extent. */
+int lmc_free_pinned_numa_ptr(uintptr_t ptr, size_t size);
+
+/* Replaces alloc_shm_pinned_ptr (csrc/common/mem_alloc.cpp:252-321; pybind
+ * csrc/pybind.cpp:352-355): creates POSIX shared-memory segment `shm_name`
+ * (exclusive create, mode 0600) of `size` bytes, reserves it in full and
+ * prefaults it, interleaved over nodes[0..n_nodes) when n_nodes > 0 (which
+ * requires the default thread memory policy).  The mapping is host memory
+ * that transfers reach through staged copies; it is not device-mapped. */
+int lmc_alloc_shm_pinned_ptr(size_t size, const char *shm_name, const int32_t *nodes,
+                             int32_t n_nodes, uintptr_t *out_ptr);
+
+/* Replaces attach_shm_pinned_ptr (csrc/common/mem_alloc.cpp:323-357; pybind
+ * csrc/pybind.cpp:356-358): maps an existing segment, read-only when
+ * writable == 0.  A segment smaller than `size` is an error. */
+int lmc_attach_shm_pinned_ptr(size_t size, const char *shm_name, int32_t writable,
+                              uintptr_t *out_ptr);
+
+/* Replaces free_shm_pinned_ptr (csrc/common/mem_alloc.cpp:359-381; pybind
+ * csrc/pybind.cpp:359-360): unmaps and unlinks the creator's mapping. */
+int lmc_free_shm_pinned_ptr(uintptr_t ptr, size_t size, const char *shm_name);
+
+/* Replaces detach_shm_pinned_ptr (csrc/common/mem_alloc.cpp:383-403; pybind
+ * csrc/pybind.cpp:361-362): unmaps a peer's mapping. */
+int lmc_detach_shm_pinned_ptr(uintptr_t ptr, size_t size);
+
+/* Replaces unlink_shm (csrc/common/mem_alloc.cpp:405-410; pybind
+ * csrc/pybind.cpp:363): removes a segment name; a missing name is not an
+ * error. */
+int lmc_unlink_shm(const char *shm_name);
+
 /* Replaces get_gpu_pci_bus_id (pybind csrc/pybind.cpp:482): the PCI bus id
  * string of `device`, written NUL-terminated into buf[0..buf_len). */
 int lmc_get_gpu_pci_bus_id(int32_t device, char *buf, int32_t buf_len);

@@ -14,6 +14,7 @@
 // buffers torch allocates with pin_memory=True, which are found even when
 // they were never recorded here.
 #include "common.h"
+#include "mem_policy.h"
 
 #include <cstring>
 #include <map>
@@ -168,6 +169,41 @@ int lmc_free_pinned_ptr(uintptr_t ptr) {
                  "alloc_pinned_ptr");
     hip_check(hipHostFree(reinterpret_cast<void *>(ptr)), "hipHostFree");
   });
+}
+
+int lmc_alloc_pinned_numa_ptr(size_t size, int32_t node, uintptr_t *out_ptr) {
+  return guarded([&] {
+    check_value(out_ptr != nullptr, "out_ptr is null");
+    check(size > 0, "alloc_pinned_numa_ptr: size must be positive");
+    check(node >= 0 && node < 1024, "NUMA node must be in [0, 1024)");
+    // The reference binds a fresh mapping to `node` and registers it
+    // (csrc/common/mem_alloc.cpp:56-92).  Here the pinned allocation itself
+    // follows the calling thread's policy (hipHostMallocNumaUser), bound to
+    // `node` for the duration of the call.
+    void *p = nullptr;
+    {
+      ScopedMemPolicy bind(MPOL_BIND, std::vector<int>{node});
+      hip_check(hipHostMalloc(&p, size,
+                              hipHostMallocPortable | hipHostMallocMapped |
+                                  hipHostMallocNumaUser),
+                "hipHostMalloc (NUMA)");
+      std::memset(p, 0, size);  // any page not placed yet lands on `node`
+    }
+    void *d = nullptr;
+    hipError_t e = hipHostGetDevicePointer(&d, p, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(p);
+      hip_check(e, "hipHostGetDevicePointer");
+    }
+    Registry::get().add(reinterpret_cast<uintptr_t>(p),
+                        reinterpret_cast<uintptr_t>(d), size, true);
+    *out_ptr = reinterpret_cast<uintptr_t>(p);
+  });
+}
+
+int lmc_free_pinned_numa_ptr(uintptr_t ptr, size_t size) {
+  (void)size;  // the allocation's own size is known to the runtime
+  return lmc_free_pinned_ptr(ptr);
 }
 
 int lmc_get_gpu_pci_bus_id(int32_t device, char *buf, int32_t buf_len) {

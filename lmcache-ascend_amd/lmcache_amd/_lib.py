@@ -92,6 +92,13 @@ SIGNATURES = {
     "lmc_unregister_ptr": [_up, ctypes.POINTER(_i32)],
     "lmc_alloc_pinned_ptr": [_sz, ctypes.c_uint32, ctypes.POINTER(_up)],
     "lmc_free_pinned_ptr": [_up],
+    "lmc_alloc_pinned_numa_ptr": [_sz, _i32, ctypes.POINTER(_up)],
+    "lmc_free_pinned_numa_ptr": [_up, _sz],
+    "lmc_alloc_shm_pinned_ptr": [_sz, ctypes.c_char_p, ctypes.POINTER(_i32), _i32, ctypes.POINTER(_up)],
+    "lmc_attach_shm_pinned_ptr": [_sz, ctypes.c_char_p, _i32, ctypes.POINTER(_up)],
+    "lmc_free_shm_pinned_ptr": [_up, _sz, ctypes.c_char_p],
+    "lmc_detach_shm_pinned_ptr": [_up, _sz],
+    "lmc_unlink_shm": [ctypes.c_char_p],
     "lmc_get_gpu_pci_bus_id": [_i32, ctypes.c_char_p, _i32],
 }
 

@@ -897,6 +897,60 @@ def free_pinned_ptr(ptr: int) -> None:
     _run(_L.lmc_free_pinned_ptr(int(ptr)))
 
 
+def alloc_pinned_numa_ptr(size: int, node: int) -> int:
+    """csrc/common/mem_alloc.cpp:56-92: zeroed pinned memory on NUMA `node`,
+    device-mapped and registered like alloc_pinned_ptr."""
+    out = ctypes.c_size_t(0)
+    _run(_L.lmc_alloc_pinned_numa_ptr(int(size), int(node), ctypes.byref(out)))
+    return int(out.value)
+
+
+def free_pinned_numa_ptr(ptr: int, size: int) -> None:
+    """csrc/common/mem_alloc.cpp:94-106."""
+    _run(_L.lmc_free_pinned_numa_ptr(int(ptr), int(size)))
+
+
+def _shm_name(shm_name) -> bytes:
+    if not isinstance(shm_name, str):
+        raise TypeError("shm_name must be a str")
+    return shm_name.encode()
+
+
+def alloc_shm_pinned_ptr(size: int, shm_name: str, interleave_nodes=()) -> int:
+    """csrc/common/mem_alloc.cpp:252-321: creates shared CPU cache slab
+    `shm_name` of `size` bytes, interleaved over `interleave_nodes`.  The
+    slab is host memory reached by staged copies (not device-mapped)."""
+    nodes = [int(n) for n in interleave_nodes]
+    arr = (ctypes.c_int32 * max(1, len(nodes)))(*nodes)
+    out = ctypes.c_size_t(0)
+    _run(_L.lmc_alloc_shm_pinned_ptr(int(size), _shm_name(shm_name), arr, len(nodes),
+                                     ctypes.byref(out)))
+    return int(out.value)
+
+
+def attach_shm_pinned_ptr(size: int, shm_name: str, writable: bool = True) -> int:
+    """csrc/common/mem_alloc.cpp:323-357."""
+    out = ctypes.c_size_t(0)
+    _run(_L.lmc_attach_shm_pinned_ptr(int(size), _shm_name(shm_name), 1 if writable else 0,
+                                      ctypes.byref(out)))
+    return int(out.value)
+
+
+def free_shm_pinned_ptr(ptr: int, size: int, shm_name: str) -> None:
+    """csrc/common/mem_alloc.cpp:359-381."""
+    _run(_L.lmc_free_shm_pinned_ptr(int(ptr), int(size), _shm_name(shm_name)))
+
+
+def detach_shm_pinned_ptr(ptr: int, size: int) -> None:
+    """csrc/common/mem_alloc.cpp:383-403."""
+    _run(_L.lmc_detach_shm_pinned_ptr(int(ptr), int(size)))
+
+
+def unlink_shm(shm_name: str) -> None:
+    """csrc/common/mem_alloc.cpp:405-410."""
+    _run(_L.lmc_unlink_shm(_shm_name(shm_name)))
+
+
 def get_gpu_pci_bus_id(device: int) -> str:
     buf = ctypes.create_string_buffer(64)
     _run(_L.lmc_get_gpu_pci_bus_id(int(device), buf, len(buf)))

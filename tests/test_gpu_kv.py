@@ -379,6 +379,65 @@ def test_alloc_pinned_and_device_ptr(ops):
     assert ops.unregister_ptr(0x7000_0000_0000) == -1
 
 
+def _first_allowed_node() -> int:
+    for line in open("/proc/self/status"):
+        if line.startswith("Mems_allowed_list:"):
+            return int(line.split(":")[1].strip().split(",")[0].split("-")[0])
+    return 0
+
+
+@pytest.mark.parametrize("direction", [True, False])
+def test_numa_pinned_host_zero_copy(ops, direction):
+    """csrc/common/mem_alloc.cpp:56-106: memory from alloc_pinned_numa_ptr on
+    a node this process may use is zeroed, registered, and the transfer kernel reads/writes it
+    through its mapped device address; freeing drops the registry record."""
+    import ctypes
+
+    gen = torch.Generator().manual_seed(140 + direction)
+    L, NB, BS, H, D, T = 2, 32, 16, 8, 128, 200
+    W = H * D
+    pbs = NB * BS
+    size = 2 * L * T * W * 2
+    p = ops.alloc_pinned_numa_ptr(size, _first_allowed_node())
+    try:
+        raw = (ctypes.c_ubyte * size).from_address(p)
+        assert not any(raw[i] for i in range(0, size, 4099))
+        assert ops.get_device_ptr(p, size) != 0
+        host = torch.frombuffer(raw, dtype=torch.bfloat16).view(2, L, T, W)
+        assert host.data_ptr() == p
+        layers = _paged(2, L, NB, BS, H, D, gen)
+        flat = _flat_tensors(layers)
+        slots = torch.tensor(sample_slots(pbs, T, seed=31), dtype=torch.int64)
+        table_np = [to_bytes(t) for t in flat]
+        if direction:
+            ops.multi_layer_kv_transfer(host, ptr_table(flat, DEV), slots.to(DEV), torch.device(DEV), pbs, True,
+                                        False, 2, W, W, 0)
+            want = np.zeros(size, np.uint8)
+            ok.multi_layer_kv_transfer(want, table_np, slots.numpy(), pbs, True, False, 2, L, W, 2)
+            _sync()
+            assert np.array_equal(to_bytes(host), want)
+        else:
+            host.copy_(randn_bf16((2, L, T, W), gen))
+            zero = [torch.zeros_like(t) for t in flat]
+            ops.multi_layer_kv_transfer(host, ptr_table(zero, DEV), slots.to(DEV), torch.device(DEV), pbs, False,
+                                        False, 2, W, W, 0)
+            zero_np = [np.zeros_like(x) for x in table_np]
+            ok.multi_layer_kv_transfer(to_bytes(host), zero_np, slots.numpy(), pbs, False, False, 2, L, W, 2)
+            _sync()
+            for z, zn in zip(zero, zero_np):
+                assert np.array_equal(to_bytes(z), zn)
+    finally:
+        ops.free_pinned_numa_ptr(p, size)
+    assert ops.get_device_ptr(p, 1) == 0
+
+
+def test_numa_pinned_bad_node_is_refused(ops):
+    with pytest.raises(RuntimeError, match="NUMA node"):
+        ops.alloc_pinned_numa_ptr(4096, 1024)
+    with pytest.raises(RuntimeError, match="set_mempolicy failed"):
+        ops.alloc_pinned_numa_ptr(4096, 1023)  # no host has 1024 NUMA nodes
+
+
 def test_unpinned_host_buffer_is_rejected(ops):
     layers = [torch.zeros((2, 8, 16, 2, 128), dtype=torch.bfloat16, device=DEV)]
     host = torch.zeros((2, 1, 16, 256), dtype=torch.bfloat16)  # pageable
