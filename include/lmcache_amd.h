@@ -404,6 +404,29 @@ int lmc_detach_shm_pinned_ptr(uintptr_t ptr, size_t size);
  * error. */
 int lmc_unlink_shm(const char *shm_name);
 
+/* One host<->device copy row: `bytes` bytes from `src` to `dst` (host
+ * addresses for the host side, device addresses for the device side). */
+typedef struct lmc_dma_segment {
+  uint64_t dst;
+  uint64_t src;
+  uint64_t bytes;
+} lmc_dma_segment;
+
+/* Replaces layerwise_prefill_dma_copy (csrc/pybind.cpp:295-310): submits
+ * copies[0..n) on `stream` (device-to-host when device_to_host != 0, else
+ * host-to-device) on the copy engines.  Rows of zero bytes are skipped.
+ * When no two destinations overlap, rows are reordered by destination,
+ * adjacent rows merged and equal-stride runs issued as one rectangular
+ * copy; otherwise rows go in the given order. */
+int lmc_layerwise_prefill_dma_copy(const lmc_dma_segment *copies, int64_t n, int32_t device_to_host,
+                                   void *stream);
+
+/* Replaces layerwise_prefill_dma_copy_diagnose (csrc/pybind.cpp:263-294):
+ * submits every row as given, one copy each, and writes each submission's
+ * host-side duration in microseconds to copy_us[i]. */
+int lmc_layerwise_prefill_dma_copy_diagnose(const lmc_dma_segment *copies, int64_t n,
+                                            int32_t device_to_host, void *stream, double *copy_us);
+
 /* Replaces get_gpu_pci_bus_id (pybind csrc/pybind.cpp:482): the PCI bus id
  * string of `device`, written NUL-terminated into buf[0..buf_len). */
 int lmc_get_gpu_pci_bus_id(int32_t device, char *buf, int32_t buf_len);

@@ -110,6 +110,18 @@ inline int64_t extent_bytes(const lmc_tensor &t) {
   return (last + 1) * elem_size(t);
 }
 
+// One pinned host allocation: [host, host + size) is mapped at dev.
+struct PinnedRange {
+  uintptr_t host;
+  size_t size;
+  uintptr_t dev;
+};
+
+// The pinned allocation holding `host`: a recorded range, or one HIP
+// reports as mapped host memory with its extent.  False for pageable or
+// unknown addresses.
+bool pinned_range(uintptr_t host, PinnedRange *out);
+
 // Host -> device address translation registry (pinned host memory).
 // Returns 0 when `host` is not inside a recorded or HIP-mapped host range of
 // at least `required` bytes.

@@ -52,6 +52,17 @@ public:
   // Returns false when no record contains `host`; otherwise true, with *dev
   // the translated address, or 0 when the record is too short for
   // `required` bytes.
+  bool range(uintptr_t host, PinnedRange *out) const {
+    std::shared_lock<std::shared_mutex> g(mu_);
+    auto it = map_.upper_bound(host);
+    if (it == map_.begin()) return false;
+    --it;
+    const Record &r = it->second;
+    if (host - r.host >= r.size) return false;
+    *out = PinnedRange{r.host, r.size, r.dev};
+    return true;
+  }
+
   bool find(uintptr_t host, size_t required, uintptr_t *dev) const {
     std::shared_lock<std::shared_mutex> g(mu_);
     auto it = map_.upper_bound(host);
@@ -84,23 +95,38 @@ thread_local std::string g_last_error;
 
 void set_last_error(const std::string &msg) { g_last_error = msg; }
 
-uintptr_t translate_host_ptr(uintptr_t host, size_t required) {
-  if (host == 0 || required == 0) return 0;
-  uintptr_t d = 0;
-  if (Registry::get().find(host, required, &d)) return d;
-  // Not recorded: ask HIP whether this is pinned (hipHostMalloc) memory.
+bool pinned_range(uintptr_t host, PinnedRange *out) {
+  if (host == 0) return false;
+  if (Registry::get().range(host, out)) return true;
+  // Not recorded: ask HIP whether this is pinned (hipHostMalloc) memory, and
+  // for the extent of its allocation.  Failed queries leave a sticky error,
+  // cleared here for the next call.
   hipPointerAttribute_t attr;
   std::memset(&attr, 0, sizeof(attr));
-  if (hipPointerGetAttributes(&attr, reinterpret_cast<void *>(host)) !=
-      hipSuccess) {
-    (void)hipGetLastError();  // clear the sticky error for the next call
-    return 0;
+  if (hipPointerGetAttributes(&attr, reinterpret_cast<void *>(host)) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
   }
-  if (attr.type != hipMemoryTypeHost || attr.devicePointer == nullptr)
-    return 0;
-  // The attribute query does not report the allocation size; the caller's
-  // required size is trusted for untracked pinned ranges.
-  return reinterpret_cast<uintptr_t>(attr.devicePointer);
+  if (attr.type != hipMemoryTypeHost || attr.devicePointer == nullptr) return false;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(host)) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  if (b > host || host - b >= size) return false;
+  // devicePointer is the mapped address of `host` itself
+  *out = PinnedRange{b, size, reinterpret_cast<uintptr_t>(attr.devicePointer) - (host - b)};
+  return true;
+}
+
+uintptr_t translate_host_ptr(uintptr_t host, size_t required) {
+  if (host == 0 || required == 0) return 0;
+  PinnedRange r;
+  if (!pinned_range(host, &r)) return 0;
+  const size_t off = host - r.host;
+  return required <= r.size - off ? r.dev + off : 0;
 }
 
 } // namespace lmc

@@ -99,6 +99,8 @@ SIGNATURES = {
     "lmc_free_shm_pinned_ptr": [_up, _sz, ctypes.c_char_p],
     "lmc_detach_shm_pinned_ptr": [_up, _sz],
     "lmc_unlink_shm": [ctypes.c_char_p],
+    "lmc_layerwise_prefill_dma_copy": [_vp, _i64, _i32, _vp],
+    "lmc_layerwise_prefill_dma_copy_diagnose": [_vp, _i64, _i32, _vp, _vp],
     "lmc_get_gpu_pci_bus_id": [_i32, ctypes.c_char_p, _i32],
 }
 

@@ -240,6 +240,14 @@ def multi_layer_kv_transfer_unilateral(*args, **kwargs):
     raise NotImplementedError("multi_layer_kv_transfer_unilateral is not implemented.")
 
 
+def multi_layer_kv_transfer_310p(*args, **kwargs):
+    """csrc/mem_kernels.cpp:215-253: the Ascend 310P's fractal (NZ) paged
+    layout, whose kernel lives outside the reference tree.  No MI355X
+    attention backend stores KV in that layout; callers reach this only when
+    the device reports itself as a 310P."""
+    raise NotImplementedError("multi_layer_kv_transfer_310p: the 310P NZ KV layout has no MI355X counterpart.")
+
+
 def _normalize_kv_caches(obj):
     # csrc/pybind.cpp:22-31: a Tensor or a tuple of Tensors.
     if isinstance(obj, torch.Tensor):
@@ -949,6 +957,42 @@ def detach_shm_pinned_ptr(ptr: int, size: int) -> None:
 def unlink_shm(shm_name: str) -> None:
     """csrc/common/mem_alloc.cpp:405-410."""
     _run(_L.lmc_unlink_shm(_shm_name(shm_name)))
+
+
+def _dma_rows(copies) -> "np.ndarray":
+    import numpy as np
+
+    rows = np.asarray(copies if len(copies) else np.empty((0, 3)), dtype=np.uint64)
+    if rows.ndim != 2 or rows.shape[1] != 3:
+        raise TypeError("copies must be a sequence of (dst, src, bytes) tuples")
+    return np.ascontiguousarray(rows)
+
+
+def layerwise_prefill_dma_copy(copies, device_to_host: bool) -> None:
+    """csrc/pybind.cpp:295-310: (dst, src, bytes) rows copied host<->device on
+    the current stream by the copy engines; rows are merged and batched when
+    no two destinations overlap."""
+    rows = _dma_rows(copies)
+    stream = torch.cuda.current_stream().cuda_stream
+    _run(_L.lmc_layerwise_prefill_dma_copy(rows.ctypes.data, rows.shape[0], 1 if device_to_host else 0, stream))
+
+
+def layerwise_prefill_dma_copy_diagnose(copies, device_to_host: bool):
+    """csrc/pybind.cpp:263-294: one copy per row; returns (stream_us,
+    stream_address, copy_us) with the host time to obtain the current stream
+    and each row's submission time, in microseconds."""
+    import time
+
+    import numpy as np
+
+    rows = _dma_rows(copies)
+    t0 = time.perf_counter()
+    stream = torch.cuda.current_stream().cuda_stream
+    stream_us = (time.perf_counter() - t0) * 1e6
+    copy_us = np.zeros(rows.shape[0], dtype=np.float64)
+    _run(_L.lmc_layerwise_prefill_dma_copy_diagnose(rows.ctypes.data, rows.shape[0], 1 if device_to_host else 0,
+                                                    stream, copy_us.ctypes.data))
+    return stream_us, int(stream or 0), copy_us.tolist()
 
 
 def get_gpu_pci_bus_id(device: int) -> str:

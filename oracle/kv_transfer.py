@@ -479,3 +479,53 @@ def indexer_c8_transfer(layers: Sequence[C8Layer], packets: Sequence[Sequence], 
                         packet[ps] = L.scales[cs]
                     else:
                         L.scales[cs] = packet[ps]
+
+
+def layerwise_dma_copy(spaces: Sequence[tuple], rows) -> None:
+    """csrc/pybind.cpp:295-310: every (dst, src, bytes) row is one memcpy,
+    applied in the given order (a later row wins where destinations
+    overlap).  `spaces` lists (base_address, flat uint8 buffer) pairs; an
+    address is resolved to the buffer whose range holds it."""
+
+    def resolve(addr: int, n: int):
+        for base, buf in spaces:
+            if base <= addr and addr + n <= base + buf.size:
+                return buf, addr - base
+        raise ValueError(f"address {addr:#x}+{n} is outside every buffer")
+
+    for dst, src, n in rows:
+        if n == 0:
+            continue
+        sbuf, so = resolve(int(src), int(n))
+        dbuf, do = resolve(int(dst), int(n))
+        dbuf[do:do + n] = sbuf[so:so + n].copy()
+
+
+def layerwise_dma_rows(chunk_addrs, chunk_tokens, cache_addrs, plane_bytes, block_ids, block_size,
+                       starts, ends, device_to_host: bool):
+    """Rows as the reference's planner binds them
+    (lmcache_ascend/v1/npu_connector/layerwise_dma.py:147-211, 558-594),
+    without its bundle-period edges: token ranges split at chunk bounds and
+    where the next block id is not the previous one plus one; for range
+    [t0, t1) of chunk c, one row per plane p with host side chunk_addrs[c] +
+    chunk_tokens[c] * (sum of the earlier planes' row bytes) + (t0 -
+    starts[c]) * plane_bytes[p], device side cache_addrs[p] + slot(t0) *
+    plane_bytes[p], and plane_bytes[p] * (t1 - t0) bytes, where slot(t) =
+    block_ids[t // block_size] * block_size + t % block_size."""
+    rows = []
+    plane_off = np.concatenate([[0], np.cumsum(plane_bytes)[:-1]])
+    for c, (s, e) in enumerate(zip(starts, ends)):
+        t = s
+        while t < e:
+            b = t // block_size
+            while (b + 1) * block_size < e and block_ids[b + 1] == block_ids[b] + 1:
+                b += 1
+            t1 = min(e, (b + 1) * block_size)
+            slot = block_ids[t // block_size] * block_size + t % block_size
+            for p, pb in enumerate(plane_bytes):
+                host = chunk_addrs[c] + chunk_tokens[c] * int(plane_off[p]) + (t - s) * pb
+                dev = cache_addrs[p] + slot * pb
+                n = (t1 - t) * pb
+                rows.append((host, dev, n) if device_to_host else (dev, host, n))
+            t = t1
+    return rows
