@@ -348,6 +348,134 @@ def bench_direct(torch, ops, dev, stream):
     return out
 
 
+def _planner_rows(pool, chunk, n_chunks, cache_addrs, plane_bytes, blocks, bs, d2h):
+    """(dst, src, bytes) rows for chunks of `chunk` tokens laid out [plane,
+    token, row] back to back from `pool`: one row per plane for every token
+    range that stays on consecutive block ids."""
+    rows = []
+    for c in range(n_chunks):
+        t, e = c * chunk, (c + 1) * chunk
+        while t < e:
+            b = t // bs
+            while (b + 1) * bs < e and blocks[b + 1] == blocks[b] + 1:
+                b += 1
+            t1 = min(e, (b + 1) * bs)
+            slot = blocks[t // bs] * bs + t % bs
+            off = 0
+            for addr, pbytes in zip(cache_addrs, plane_bytes):
+                host = pool + c * chunk * sum(plane_bytes) + chunk * off + (t - c * chunk) * pbytes
+                dev = addr + slot * pbytes
+                rows.append((host, dev, (t1 - t) * pbytes) if d2h else (dev, host, (t1 - t) * pbytes))
+                off += pbytes
+            t = t1
+    return rows
+
+
+def bench_layerwise_dma(torch, ops, dev, stream):
+    """Layerwise prefill copies of one Llama-shape SEPARATE_KV layer (8 x 128
+    bf16 per plane, 2048 blocks of 128 tokens): 4096 tokens in 16 memory
+    objects of 256 tokens carved from one pinned pool, rows bound as the
+    connector's planner binds them, for scattered and for consecutive block
+    ids, both directions.  The one-copy-per-row submission the reference
+    uses is timed beside it."""
+    T, CS, BS, NB, W = 4096, 256, 128, 2048, 1024
+    pb = [W * ES, W * ES]
+    pool = torch.empty(T * sum(pb), dtype=torch.uint8, pin_memory=True)
+    caches = [torch.empty(NB * BS * b, dtype=torch.uint8, device=dev) for b in pb]
+    nch = T // CS
+    gen = torch.Generator().manual_seed(17)
+    out = {}
+    for layout in ("scattered", "consecutive"):
+        blocks = (torch.randperm(NB, generator=gen)[:T // BS] if layout == "scattered"
+                  else torch.arange(64, 64 + T // BS)).tolist()
+        for d2h in (False, True):
+            rows = _planner_rows(pool.data_ptr(), CS, nch, [c.data_ptr() for c in caches], pb, blocks, BS, d2h)
+            nbytes = sum(r[2] for r in rows)
+            ours = lambda: ops.layerwise_prefill_dma_copy(rows, d2h)
+            per_row = lambda: ops.layerwise_prefill_dma_copy_diagnose(rows, d2h)
+            ours(); per_row()
+            t_o = statistics.median(time_events(torch, stream, ours, 20)[0] for _ in range(3))
+            t_p = time_events(torch, stream, per_row, 10)[0]
+            name = f"layerwise_dma_{'store' if d2h else 'load'}_{layout}_llama_layer"
+            out[name] = {"ms": round(t_o, 4), "rows": len(rows), "payload_GBps": round(nbytes / t_o / 1e6, 2),
+                         "pcie_frac": round(nbytes / t_o / 1e6 / PCIE_PEAK_GBS, 4),
+                         "per_row_copies_GBps": round(nbytes / t_p / 1e6, 2)}
+    torch.cuda.synchronize()
+    del pool, caches
+    return out
+
+
+def bench_c8_graph(torch, ops, dev, stream):
+    """DeepSeek-V3.2-shape sparse-attention side paths.  Indexer C8: 8
+    layers of int8 keys [2048 blocks, 128, 1, 128] with float16 scales,
+    16384 prefill tokens in 16 packets of 1024 per layer at block-scattered
+    slots, packed into device packets (HBM) and into pinned packets (PCIe),
+    and unpacked back.  Sparse graph copy: 64 requests x 2048 selected tokens
+    of an MLA layer (512 + 64 bf16) from device chunk sources of 256
+    tokens into distinct cache slots (HBM)."""
+    L, NB, T, CC = 8, 2048, 16384, 1024
+    gen = torch.Generator().manual_seed(23)
+    keys = [torch.randint(-128, 127, (NB, 128, 1, 128), dtype=torch.int8, generator=gen).to(dev) for _ in range(L)]
+    scales = [torch.randn((NB, 128, 1, 1), generator=gen).to(torch.float16).to(dev) for _ in range(L)]
+    state = ops.IndexerC8GroupState([ops.IndexerC8State(k, s) for k, s in zip(keys, scales)])
+    blocks = torch.randperm(NB, generator=gen)[:T // 128]
+    slots = (blocks[:, None] * 128 + torch.arange(128)).reshape(-1).to(dev)
+    nch = T // CC
+    offs = torch.arange(0, T, CC, dtype=torch.int32, device=dev)
+    cnts = torch.full((nch,), CC, dtype=torch.int32, device=dev)
+    nbytes = L * T * 130
+    out = {}
+    for where in ("device", "pinned"):
+        if where == "device":
+            pk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        else:
+            pk = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        base = pk.data_ptr() if where == "device" else ops.get_device_ptr(pk.data_ptr(), nbytes)
+        if base == 0:
+            raise RuntimeError("pinned packet buffer is not device-mapped")
+        ptrs = torch.tensor([[base + (l * T + c * CC) * 130 for c in range(nch)] for l in range(L)],
+                            dtype=torch.int64, device=dev)
+        pack = lambda: ops.indexer_c8_group_transfer_prepared(state, ptrs, offs, cnts, slots, CC, True)
+        unpack = lambda: ops.indexer_c8_group_transfer_prepared(state, ptrs, offs, cnts, slots, CC, False)
+        pack(); unpack()
+        t_p = time_events(torch, stream, pack, 20)[0]
+        t_u = time_events(torch, stream, unpack, 20)[0]
+        for name, t in (("pack", t_p), ("unpack", t_u)):
+            e = {"ms": round(t, 4), "payload_GBps": round(nbytes / t / 1e6, 2)}
+            if where == "device":
+                e["hbm_frac"] = round(2 * nbytes / t / 1e6 / HBM_PEAK_GBS, 4)
+            else:
+                e["pcie_frac"] = round(nbytes / t / 1e6 / PCIE_PEAK_GBS, 4)
+            out[f"indexer_c8_{name}_{where}_8x16k"] = e
+        del pk
+    # sparse graph copy
+    R, Wsel, CS, KH, PH = 64, 2048, 256, 512, 64
+    MB, BSZ = 4096, 64
+    k = torch.zeros((MB, BSZ, 1, KH), dtype=torch.bfloat16, device=dev)
+    pe = torch.zeros((MB, BSZ, 1, PH), dtype=torch.bfloat16, device=dev)
+    limit = 8192
+    cpr = limit // CS
+    src_k = torch.randn((R * cpr, CS, KH), generator=gen).to(torch.bfloat16).to(dev)
+    src_p = torch.randn((R * cpr, CS, PH), generator=gen).to(torch.bfloat16).to(dev)
+    ptrs = torch.stack([src_k.data_ptr() + torch.arange(R * cpr, dtype=torch.int64) * CS * KH * ES,
+                        src_p.data_ptr() + torch.arange(R * cpr, dtype=torch.int64) * CS * PH * ES]).to(dev)
+    sel = torch.stack([torch.randperm(limit, generator=gen)[:Wsel] for _ in range(R)]).to(torch.int32).to(dev)
+    gslots = torch.randperm(MB * BSZ, generator=gen)[:R * Wsel].reshape(R, Wsel).to(dev)
+    counts = torch.full((R,), Wsel, dtype=torch.int32, device=dev)
+    limits = torch.full((R,), limit, dtype=torch.int32, device=dev)
+    st = ops.prepare_sparse_direct_destination_state((k, pe), torch.zeros(1, device=dev), 5, 0, 0, 0)
+    graph = lambda: ops.sparse_graph_kv_transfer(st, gslots, sel, counts, ptrs, limits, CS)
+    graph()
+    t_g = time_events(torch, stream, graph, 20)[0]
+    gbytes = R * Wsel * (KH + PH) * ES
+    out["sparse_graph_copy_mla_64x2048"] = {"ms": round(t_g, 4), "payload_GBps": round(gbytes / t_g / 1e6, 1),
+                                            "hbm_frac": round(2 * gbytes / t_g / 1e6 / HBM_PEAK_GBS, 4)}
+    torch.cuda.synchronize()
+    del keys, scales, state, k, pe, src_k, src_p
+    torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,7 +483,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct",
+    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct,dma,c8graph",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -531,6 +659,10 @@ def main(argv=None):
         extra_big.update(bench_mla_576(torch, ops, dev, stream))
     if "direct" in sel:
         extra_big.update(bench_direct(torch, ops, dev, stream))
+    if "dma" in sel:
+        extra_big.update(bench_layerwise_dma(torch, ops, dev, stream))
+    if "c8graph" in sel:
+        extra_big.update(bench_c8_graph(torch, ops, dev, stream))
 
     def gbs(nbytes, ms):
         return round(nbytes / (ms * 1e-3) / 1e9, 2)

@@ -809,7 +809,7 @@ class IndexerC8State:
     """One layer's indexer cache: float16/bfloat16 keys [NB, 128, 1, 128],
     or int8 keys with float16 scales [NB, 128, 1, 1]; physical slot factor
     1 (or 2 for int8) or an int32 block permutation (csrc/indexer_c8.cpp:
-    13-50)."""
+    13-50).  The layer's descriptors are built once, here."""
 
     def __init__(self, keys, scales=None, slot_factor=1, block_map=None):
         kd = _desc(keys)
@@ -821,6 +821,13 @@ class IndexerC8State:
         self.slot_factor = int(slot_factor)
         self.cache_slots = keys.numel() // 128 // self.slot_factor
         self.key_bytes = 128 * keys.element_size()
+        self._descs = (kd, sd, md)
+        self._table = None
+
+    def _layer_table(self):
+        if self._table is None:
+            self._table = _c8_table([self])
+        return self._table
 
 
 class IndexerC8GroupState:
@@ -835,20 +842,27 @@ class IndexerC8GroupState:
                 raise RuntimeError("C8 group layers must share device and slot capacity")
         self.layers = layers
         self.max_key_bytes = max([128] + [st.key_bytes for st in layers])
+        self._table = _c8_table(layers)
+
+    def _layer_table(self):
+        return self._table
 
 
-def _c8(layers, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu, fixed_chunks):
+def _c8_table(layers):
+    """ctypes arrays of the layers' key / scale / block-map descriptors and
+    slot factors, with the device index; they keep the descriptors alive."""
     n = len(layers)
-    keys = [_desc(st.keys) for st in layers]
-    scales = [_desc(st.scales) if st.scales is not None else None for st in layers]
-    maps = [_desc(st.block_map) if st.block_map is not None else None for st in layers]
     P = ctypes.POINTER(_lib.LmcTensor)
-    ka = (P * n)(*[ctypes.pointer(x) for x in keys])
-    sa = (P * n)(*[ctypes.pointer(x) if x is not None else P() for x in scales])
-    ma = (P * n)(*[ctypes.pointer(x) if x is not None else P() for x in maps])
+    ka = (P * n)(*[ctypes.pointer(st._descs[0]) for st in layers])
+    sa = (P * n)(*[ctypes.pointer(st._descs[1]) if st._descs[1] is not None else P() for st in layers])
+    ma = (P * n)(*[ctypes.pointer(st._descs[2]) if st._descs[2] is not None else P() for st in layers])
     fa = (ctypes.c_int64 * n)(*[st.slot_factor for st in layers])
+    return ka, sa, ma, fa, n, _device_index(layers[0].keys)
+
+
+def _c8(table, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu, fixed_chunks):
+    ka, sa, ma, fa, n, dev = table
     d = [_desc(x) for x in (packet_ptrs, chunk_offsets, chunk_counts, slot_mapping)]
-    dev = _device_index(layers[0].keys)
     _run(
         _L.lmc_indexer_c8_transfer(
             ka, sa, ma, fa, n, *[_ref(x) for x in d], int(chunk_capacity), int(bool(from_npu)),
@@ -860,13 +874,14 @@ def _c8(layers, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_ca
 def indexer_c8_transfer_prepared(state, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity,
                                  from_npu, fixed_chunks=False) -> None:
     """csrc/indexer_c8.cpp:139-158."""
-    _c8([state], packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu, fixed_chunks)
+    _c8(state._layer_table(), packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu,
+        fixed_chunks)
 
 
 def indexer_c8_group_transfer_prepared(state, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping,
                                        chunk_capacity, from_npu, fixed_chunks=False) -> None:
     """csrc/indexer_c8.cpp:160-184: packet_ptrs is [layers, chunks]."""
-    _c8(state.layers, packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu,
+    _c8(state._layer_table(), packet_ptrs, chunk_offsets, chunk_counts, slot_mapping, chunk_capacity, from_npu,
         fixed_chunks)
 
 
