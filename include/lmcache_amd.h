@@ -139,7 +139,7 @@ int lmc_single_layer_kv_transfer(const lmc_tensor *lmc_key_value_cache,
                                  int64_t k_hidden_dims, int64_t v_hidden_dims,
                                  int64_t dsa_hidden_dims, void *stream);
 
-/* Replaces load_and_reshape_flash (csrc/mem_kernels.cpp:1341-1387; pybind
+/* Replaces load_and_reshape_flash (csrc/mem_kernels.cpp:1341-1389; pybind
  * csrc/pybind.cpp:475): layer `layer_idx` of key_value [2, L, T, W] is
  * filled from key_cache / value_cache rows slot_mapping[t]. */
 int lmc_load_and_reshape_flash(const lmc_tensor *key_value,
@@ -148,7 +148,7 @@ int lmc_load_and_reshape_flash(const lmc_tensor *key_value,
                                const lmc_tensor *slot_mapping,
                                int32_t layer_idx, void *stream);
 
-/* Replaces reshape_and_cache_back_flash (csrc/mem_kernels.cpp:1389-1440;
+/* Replaces reshape_and_cache_back_flash (csrc/mem_kernels.cpp:1391-1440;
  * pybind csrc/pybind.cpp:476): the inverse of lmc_load_and_reshape_flash. */
 int lmc_reshape_and_cache_back_flash(const lmc_tensor *key_value,
                                      const lmc_tensor *key_cache,
@@ -160,7 +160,7 @@ int lmc_reshape_and_cache_back_flash(const lmc_tensor *key_value,
  * Sparse, direct and staged-batch single-layer transfers
  * ------------------------------------------------------------------------ */
 
-/* Replaces sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:415-497;
+/* Replaces sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:418-497;
  * pybind csrc/pybind.cpp:381-387): retrieve only, for each i
  * paged[slot_mapping_packed[i]] = LMC token selected_token_idx[i] of the
  * single-layer buffer (layout as lmc_single_layer_kv_transfer).  Both index
@@ -174,7 +174,7 @@ int lmc_sparse_single_layer_kv_transfer(
     int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
 
 /* Replaces sparse_mla_dsa_batched_direct_kv_transfer and its _fast /
- * _prepared forms (csrc/mem_kernels.cpp:584-1059; pybind csrc/pybind.cpp:
+ * _prepared forms (csrc/mem_kernels.cpp:588-752, 833-976; pybind csrc/pybind.cpp:
  * 397-436): retrieve from memory objects reached through the device table
  * chunk_ptrs (int64, one kernel-visible address per chunk).  Entry i moves
  * token selected_token_idx[i] (chunk = token / chunk_size, n_c = min(
@@ -197,7 +197,7 @@ int lmc_sparse_direct_kv_transfer(
     int32_t validate_inputs, void *stream);
 
 /* Replaces dense_mla_dsa_batched_direct_kv_transfer and its _fast /
- * _prepared / group forms (csrc/mem_kernels.cpp:1131-1289; pybind
+ * _prepared / group forms (csrc/mem_kernels.cpp:978-1306; pybind
  * csrc/pybind.cpp:441-472, 312-327), MLA/DSA formats: token g in
  * [0, numel(slot_mapping_full)) belongs to chunk g / fixed_chunk_size, or
  * (fixed_chunk_size == 0) to the chunk c with chunk_offsets[c] <= g <
@@ -229,7 +229,7 @@ int lmc_batched_fused_single_layer_kv_transfer(
     int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
 
 /* Replaces batched_fused_sparse_single_layer_kv_transfer
- * (csrc/mem_kernels.cpp:1291-1339; pybind csrc/pybind.cpp:388-396):
+ * (csrc/mem_kernels.cpp:1308-1339; pybind csrc/pybind.cpp:388-396):
  * objects -> staging, then lmc_sparse_single_layer_kv_transfer from the
  * staging buffer. */
 int lmc_batched_fused_sparse_single_layer_kv_transfer(
@@ -242,7 +242,7 @@ int lmc_batched_fused_sparse_single_layer_kv_transfer(
     void *stream);
 
 /* Replaces sparse_graph_kv_transfer and its sfa_copy kernels
- * (csrc/mem_kernels.cpp:742-831; csrc/graph/sparse_graph_kernel.cpp:6-132;
+ * (csrc/mem_kernels.cpp:754-831; csrc/graph/sparse_graph_kernel.cpp:6-132;
  * pybind csrc/pybind.cpp:437-440): entry (r, j) of the packed
  * [requests, row_width] `selected` / `slots` matrices, active for j <
  * min(counts[r * stride(0)], row_width) when counts and limits[r] are > 0,

@@ -412,7 +412,7 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   const lmc_tensor &slots = index_tensor(slots_t, "slot_mapping_packed");
   const lmc_tensor &sel = index_tensor(sel_t, "selected_token_idx");
   if (validate) validate_sparse_inputs(slots, sel);
-  // csrc/mem_kernels.cpp:604-606, 734-739.
+  // csrc/mem_kernels.cpp:601-602, 692-693.
   check(chunk_size > 0, "chunk_size must be positive.");
   check(total_tokens > 0, "total_tokens must be positive.");
   check(chunk_size < (int64_t(1) << 31) && total_tokens < (int64_t(1) << 31),
@@ -435,7 +435,7 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   set_sparse_indices(job, slots, sel);
   if (job.n_entries == 0) return;
   if (counts_t != nullptr) {
-    // Count-aware rows (csrc/mem_kernels.cpp:641-649): selected tokens form
+    // Count-aware rows (csrc/mem_kernels.cpp:636-650): selected tokens form
     // rows of num_sparse / requests entries; row r holds counts[r] valid
     // entries, the rest is padding.
     const lmc_tensor &counts = deref(counts_t, "selected_token_counts");
@@ -456,7 +456,7 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   launch_entries(job, true, stream);
 }
 
-// csrc/mem_kernels.cpp:1061-1129, with the reference's messages.
+// csrc/mem_kernels.cpp:978-1034, with the reference's messages.
 void validate_dense_inputs(const lmc_tensor &slots, const lmc_tensor &ptrs,
                            const lmc_tensor &offs, const lmc_tensor &sizes,
                            int64_t total_tokens, int64_t fixed) {
@@ -528,7 +528,7 @@ void dense_direct(const lmc_tensor *ptrs_t, const lmc_tensor *caches, int n,
   launch_entries(job, true, stream);
 }
 
-// --- staged batched paths (csrc/mem_kernels.cpp:336-413, 1291-1339;
+// --- staged batched paths (csrc/mem_kernels.cpp:336-416, 1308-1339;
 //     host copies csrc/utils.cpp:500-733) -----------------------------------
 
 void copy_async(void *dst, const void *src, int64_t bytes, hipStream_t s) {

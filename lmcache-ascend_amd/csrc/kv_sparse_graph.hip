@@ -1,6 +1,6 @@
 // Sparse-attention KV copy for graph replay ("sfa_copy") on MI355X (gfx950).
 //
-// Replaces sparse_graph_kv_transfer (csrc/mem_kernels.cpp:742-831; device
+// Replaces sparse_graph_kv_transfer (csrc/mem_kernels.cpp:754-831; device
 // semantics csrc/graph/sparse_graph_kernel.cpp:6-72).  Requests are rows of
 // a packed [requests, row_width] matrix of selected tokens and destination
 // slots; row r is active for its first min(counts[r * stride], row_width)
@@ -99,7 +99,7 @@ bool contiguous(const lmc_tensor &t) {
   return true;
 }
 
-// csrc/mem_kernels.cpp:746-795, with the reference's messages.
+// csrc/mem_kernels.cpp:758-800, with the reference's messages.
 void sparse_graph(const lmc_tensor &k, const lmc_tensor &pe, int64_t kH, int64_t peH,
                   const lmc_tensor &slots, const lmc_tensor &sel, const lmc_tensor &counts,
                   const lmc_tensor &ptrs, const lmc_tensor &limits, int64_t chunk_size,

@@ -304,7 +304,7 @@ def _single_layer_kv_transfer_ctypes(
 
 
 def load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, layer_idx) -> None:
-    """csrc/mem_kernels.cpp:1341-1387: key_value[:, layer_idx] <- paged rows."""
+    """csrc/mem_kernels.cpp:1341-1389: key_value[:, layer_idx] <- paged rows."""
     if _ext is not None:
         _ext.load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, int(layer_idx))
         return
@@ -314,7 +314,7 @@ def load_and_reshape_flash(key_value, key_cache, value_cache, slot_mapping, laye
 
 
 def reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping, layer_idx) -> None:
-    """csrc/mem_kernels.cpp:1389-1440: paged rows <- key_value[:, layer_idx]."""
+    """csrc/mem_kernels.cpp:1391-1440: paged rows <- key_value[:, layer_idx]."""
     if _ext is not None:
         _ext.reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping, int(layer_idx))
         return
@@ -417,7 +417,7 @@ def _check_caches(caches, fmt, two_major=False, kH=0, vH=0, dsaH=0) -> None:
 
 def _chunk_ptrs_for(lmc_tensors, device) -> torch.Tensor:
     """Device int64 table of the memory objects' kernel-visible addresses
-    (csrc/mem_kernels.cpp:615-628)."""
+    (csrc/mem_kernels.cpp:618-633)."""
     ptrs = []
     for t in lmc_tensors:
         if t.is_cuda:
@@ -470,7 +470,7 @@ def sparse_single_layer_kv_transfer(
     token_major=False, vllm_two_major=False, k_hidden_dims=0, v_hidden_dims=0, dsa_hidden_dims=0,
 ) -> None:
     """Retrieve only: paged[slot_mapping_packed[i]] = LMC[selected_token_idx[i]]
-    (csrc/mem_kernels.cpp:415-497; tests/v1/test_mem_kernels.py:1445-1543)."""
+    (csrc/mem_kernels.cpp:418-497; tests/v1/test_mem_kernels.py:1445-1543)."""
     caches = _normalize_kv_caches(vllm_kv_caches)
     arr = _cache_array(caches)
     dev = _device_index(*(caches + [slot_mapping_packed]))
@@ -489,7 +489,7 @@ def batched_fused_single_layer_kv_transfer(
     dsa_hidden_dims=0,
 ) -> None:
     """Single-layer copy through `staging_cache` plus one DMA copy per chunk
-    and plane (csrc/mem_kernels.cpp:336-413; tests/v1/test_mem_kernels.py:
+    and plane (csrc/mem_kernels.cpp:336-416; tests/v1/test_mem_kernels.py:
     791-1062).  direction True: paged -> staging -> lmc_tensors."""
     caches = _normalize_kv_caches(vllm_kv_caches)
     arr = _cache_array(caches)
@@ -513,7 +513,7 @@ def batched_fused_sparse_single_layer_kv_transfer(
     v_hidden_dims=0, dsa_hidden_dims=0, sparse_indices_cpu=None,
 ) -> None:
     """lmc_tensors -> staging, then sparse_single_layer_kv_transfer from the
-    staging buffer (csrc/mem_kernels.cpp:1291-1339).  `sparse_indices_cpu`
+    staging buffer (csrc/mem_kernels.cpp:1308-1339).  `sparse_indices_cpu`
     only steers the reference's choice of per-token copies; every chunk is
     staged whole here."""
     caches = _normalize_kv_caches(vllm_kv_caches)
@@ -601,7 +601,7 @@ def sparse_mla_dsa_batched_direct_kv_transfer(
     dsa_hidden_dims=0, lmc_host_interleaved=False, chunk_ptrs_npu=None, selected_token_counts=None,
 ) -> None:
     """Retrieve selected tokens straight from pinned memory objects
-    (csrc/mem_kernels.cpp:584-672; tools/cpu_vllm_runtime.py:288-343)."""
+    (csrc/mem_kernels.cpp:588-682; tools/cpu_vllm_runtime.py:288-343)."""
     caches = _normalize_kv_caches(vllm_kv_caches)
     _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
     if int(chunk_size) <= 0:
@@ -626,7 +626,7 @@ def sparse_mla_dsa_batched_direct_kv_transfer_fast(
     layer_state, slot_mapping_packed, selected_token_idx, chunk_ptrs_npu, chunk_size, total_tokens,
     lmc_host_interleaved, validate_inputs=False, selected_token_counts=None,
 ) -> None:
-    """csrc/mem_kernels.cpp:674-738."""
+    """csrc/mem_kernels.cpp:684-752."""
     st = layer_state
     if selected_token_idx.numel() == 0 and not validate_inputs:
         return
@@ -640,7 +640,7 @@ def sparse_mla_dsa_batched_direct_kv_transfer_prepared(
     destination_state, slot_mapping_packed, selected_token_idx, chunk_ptrs_npu, chunk_size, total_tokens,
     lmc_host_interleaved, selected_token_counts=None, diagnostic_layer_id=-1,
 ) -> None:
-    """csrc/mem_kernels.cpp:833-949 (the diagnostic timing is not kept)."""
+    """csrc/mem_kernels.cpp:833-976 (the diagnostic timing is not kept)."""
     st = destination_state
     if selected_token_idx.numel() == 0:
         return
@@ -670,7 +670,7 @@ def dense_mla_dsa_batched_direct_kv_transfer(
     dsa_hidden_dims=0, lmc_host_interleaved=False, direction=False, chunk_ptrs_npu=None, fixed_chunk_size=0,
 ) -> None:
     """Every token of each memory object, either direction
-    (csrc/mem_kernels.cpp:1131-1186; tools/cpu_vllm_runtime.py:353-411)."""
+    (csrc/mem_kernels.cpp:1036-1114; tools/cpu_vllm_runtime.py:353-411)."""
     caches = _normalize_kv_caches(vllm_kv_caches)
     _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
     if int(kvcache_format_raw) not in _MLA_DSA:
@@ -690,7 +690,7 @@ def dense_mla_dsa_batched_direct_kv_transfer_fast(
     layer_state, slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
     lmc_host_interleaved, direction, validate_inputs=False, fixed_chunk_size=0,
 ) -> None:
-    """csrc/mem_kernels.cpp:1188-1231."""
+    """csrc/mem_kernels.cpp:1116-1166."""
     st = layer_state
     _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
                   slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
@@ -701,7 +701,7 @@ def dense_mla_dsa_batched_direct_kv_transfer_prepared(
     destination_state, slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
     lmc_host_interleaved, validate_inputs=False, fixed_chunk_size=0,
 ) -> None:
-    """Retrieve (memory objects -> paged), csrc/mem_kernels.cpp:1233-1277."""
+    """Retrieve (memory objects -> paged), csrc/mem_kernels.cpp:1168-1219."""
     st = destination_state
     _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
                   slot_mapping_full, chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu, total_tokens,
@@ -711,7 +711,7 @@ def dense_mla_dsa_batched_direct_kv_transfer_prepared(
 def _dense_group(layer_states, slot_mapping_full, layer_chunk_ptrs_npu, chunk_offsets_npu, chunk_sizes_npu,
                  total_tokens, lmc_host_interleaved, direction, validate_inputs, fixed_chunk_size):
     """One dense direct transfer per layer, layer l using row l of the
-    [layers, chunks] pointer table (csrc/mem_kernels.cpp:1279-1339)."""
+    [layers, chunks] pointer table (csrc/mem_kernels.cpp:1221-1306)."""
     if len(layer_states) == 0:
         raise RuntimeError("layer_states must not be empty.")
     if layer_chunk_ptrs_npu.dim() != 2:
@@ -782,7 +782,7 @@ def dense_mla_dsa_group_direct_kv_transfer_prepared(
 def sparse_graph_kv_transfer(destination_state, slots, selected, counts, ptrs, limits, chunk_size,
                              max_aiv_cores=0) -> None:
     """Graph-replay sparse copy into a prepared MLA destination
-    (csrc/mem_kernels.cpp:742-831; csrc/graph/sparse_graph_kernel.cpp):
+    (csrc/mem_kernels.cpp:754-831; csrc/graph/sparse_graph_kernel.cpp):
     rows of `selected` / `slots` per request, `counts` and `limits` per row,
     `ptrs` the [2, requests * chunks] K and PE chunk-source tables."""
     st = destination_state

@@ -226,7 +226,7 @@ def sparse_single_layer_kv_transfer(lmc: TensorBytes, caches: List[TensorBytes],
                                     slots_packed: np.ndarray, selected: np.ndarray, fmt: int,
                                     token_major: bool = False, vllm_two_major: bool = False,
                                     kH: int = 0, vH: int = 0, dsaH: int = 0) -> None:
-    """sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:415-497;
+    """sparse_single_layer_kv_transfer (csrc/mem_kernels.cpp:418-497;
     tests/v1/test_mem_kernels.py:1445-1543): for each i, paged row
     slots_packed[i] <- LMC token selected[i]; entries whose slot or token is
     out of range are skipped."""
@@ -298,7 +298,7 @@ def sparse_direct_kv_transfer(chunks: Sequence[np.ndarray], caches: List[TensorB
     CPU restatement (tools/cpu_vllm_runtime.py:288-343): entry i moves token
     selected[i] (chunk selected[i] // chunk_size, n_c = min(chunk_size,
     total_tokens - chunk * chunk_size)) into paged row slots_packed[i].
-    `counts` (csrc/mem_kernels.cpp:641-649): the entries form len(counts)
+    `counts` (csrc/mem_kernels.cpp:636-650): the entries form len(counts)
     rows of equal width; only the first counts[r] of row r are valid.
     MERGED/SEPARATE memory objects have the layout of `layout` (shape and
     strides of the first chunk)."""
