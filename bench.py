@@ -378,6 +378,7 @@ def bench_layerwise_dma(torch, ops, dev, stream):
     connector's planner binds them, for scattered and for consecutive block
     ids, both directions.  The one-copy-per-row submission the reference
     uses is timed beside it."""
+    torch.cuda.empty_cache()  # fresh allocations, not blocks cached by earlier modes
     T, CS, BS, NB, W = 4096, 256, 128, 2048, 1024
     pb = [W * ES, W * ES]
     pool = torch.empty(T * sum(pb), dtype=torch.uint8, pin_memory=True)
@@ -413,6 +414,7 @@ def bench_c8_graph(torch, ops, dev, stream):
     and unpacked back.  Sparse graph copy: 64 requests x 2048 selected tokens
     of an MLA layer (512 + 64 bf16) from device chunk sources of 256
     tokens into distinct cache slots (HBM)."""
+    torch.cuda.empty_cache()  # fresh allocations, not blocks cached by earlier modes
     L, NB, T, CC = 8, 2048, 16384, 1024
     gen = torch.Generator().manual_seed(23)
     keys = [torch.randint(-128, 127, (NB, 128, 1, 128), dtype=torch.int8, generator=gen).to(dev) for _ in range(L)]
@@ -470,8 +472,22 @@ def bench_c8_graph(torch, ops, dev, stream):
     gbytes = R * Wsel * (KH + PH) * ES
     out["sparse_graph_copy_mla_64x2048"] = {"ms": round(t_g, 4), "payload_GBps": round(gbytes / t_g / 1e6, 1),
                                             "hbm_frac": round(2 * gbytes / t_g / 1e6 / HBM_PEAK_GBS, 4)}
+    # the same selections from chunk sources in pinned host memory (PCIe)
+    hk = src_k.cpu().pin_memory()
+    hp = src_p.cpu().pin_memory()
+    hkd, hpd = ops.get_device_ptr(hk.data_ptr(), hk.numel() * ES), ops.get_device_ptr(hp.data_ptr(), hp.numel() * ES)
+    if hkd == 0 or hpd == 0:
+        raise RuntimeError("pinned chunk sources are not device-mapped")
+    hptrs = torch.stack([hkd + torch.arange(R * cpr, dtype=torch.int64) * CS * KH * ES,
+                         hpd + torch.arange(R * cpr, dtype=torch.int64) * CS * PH * ES]).to(dev)
+    hgraph = lambda: ops.sparse_graph_kv_transfer(st, gslots, sel, counts, hptrs, limits, CS)
+    hgraph()
+    t_h = time_events(torch, stream, hgraph, 10)[0]
+    out["sparse_graph_copy_mla_64x2048_pinned_sources"] = {
+        "ms": round(t_h, 4), "payload_GBps": round(gbytes / t_h / 1e6, 2),
+        "pcie_frac": round(gbytes / t_h / 1e6 / PCIE_PEAK_GBS, 4)}
     torch.cuda.synchronize()
-    del keys, scales, state, k, pe, src_k, src_p
+    del keys, scales, state, k, pe, src_k, src_p, hk, hp
     torch.cuda.empty_cache()
     return out
 

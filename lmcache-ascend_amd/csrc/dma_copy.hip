@@ -14,17 +14,19 @@
 //   1. rows are ordered by their device-side address (each plane's cache is
 //      one allocation, so its rows stay together);
 //   2. rows adjacent in both address spaces are merged;
-//   3. runs of four or more equal-length rows at constant destination and
-//      source pitches become one rectangular copy on the copy engines;
-//   4. the remaining rows whose host side lies in pinned, device-mapped
-//      memory are copied by one small kernel (a capped grid, so a prefill
-//      running beside it keeps nearly every compute unit), 64 rows per
-//      launch with the row table in the kernel arguments;
-//   5. rows over pageable host memory, and rows of 4 MiB or more, go to the
-//      copy engines one by one.
-// With overlapping destinations the rows are submitted in the caller's
-// order on the copy engines, merging only consecutive adjacent rows, which
-// keeps the last-writer-wins result of the reference.
+//   3. rows whose host side lies in pinned, device-mapped memory are copied
+//      by one small kernel (at most 64 workgroups, so a prefill running
+//      beside it keeps nearly every compute unit), 64 rows per launch with
+//      the row table in the kernel arguments;
+//   4. rows over pageable host memory, and rows of 4 MiB or more, go to the
+//      copy engines: runs of four or more equal-length rows at constant
+//      pitches as one rectangular copy, the rest one by one.
+// Rectangular copies between device and pinned memory were measured at
+// 53 GB/s on a fresh process but 20 GB/s after a long run of other work,
+// while the kernel held 54 GB/s in both; pinned rows therefore always take
+// the kernel.  With overlapping destinations the rows are submitted in the
+// caller's order on the copy engines, merging only consecutive adjacent
+// rows, which keeps the last-writer-wins result of the reference.
 #include "common.h"
 
 #include <algorithm>
@@ -209,54 +211,60 @@ void dma_copy(const lmc_dma_segment *rows, int64_t n, bool d2h, hipStream_t stre
     std::stable_sort(sorted.begin(), sorted.end(), [](const Seg &a, const Seg &b) { return a.src < b.src; });
   for (const Seg &s : sorted) push_merged(merged, s);
 
+  // Rows over pinned, device-mapped host memory go to the copy kernel;
+  // rows over pageable memory, and rows of kEngineRowBytes or more, to the
+  // copy engines.
+  std::vector<PinnedRange> seen;
+  std::vector<Seg> kernel_rows;  // device-visible addresses on both sides
+  std::vector<Seg> kernel_orig;  // the same rows as given
+  std::vector<Seg> engine_rows;
+  for (const Seg &s : merged) {
+    const uint64_t h = d2h ? s.dst : s.src;
+    const uint64_t dev = s.bytes < kEngineRowBytes ? mapped(h, s.bytes, seen) : 0;
+    if (dev == 0) {
+      engine_rows.push_back(s);
+      continue;
+    }
+    kernel_rows.push_back(d2h ? Seg{dev, s.src, s.bytes} : Seg{s.dst, dev, s.bytes});
+    kernel_orig.push_back(s);
+  }
+  // one row alone gains nothing from a launch over a copy-engine copy
+  if (kernel_rows.size() == 1)
+    engine_rows.push_back(kernel_orig[0]);
+  else if (!kernel_rows.empty())
+    launch_rows(kernel_rows, stream);
+  if (engine_rows.empty()) return;
+
   const uint64_t max_pitch = device_max_pitch();
   // A run needs both pitches positive and at least one row long, so that
-  // neither its destination rows nor its source rows overlap.
+  // neither its destination rows nor its source rows overlap.  Runs shorter
+  // than kMinRun rows cost the copy engines as much as their rows one by
+  // one.
   auto pitch_ok = [&](const Seg &p, const Seg &q, uint64_t *dp, uint64_t *sp) {
     if (q.bytes != p.bytes || q.dst <= p.dst || q.src <= p.src) return false;
     *dp = q.dst - p.dst;
     *sp = q.src - p.src;
     return *dp >= p.bytes && *sp >= p.bytes && *dp <= max_pitch && *sp <= max_pitch;
   };
-  // Runs shorter than kMinRun rows cost the copy engines as much as their
-  // rows would one by one; their rows stay singles.
-  std::vector<Seg> singles;
   size_t i = 0;
-  while (i < merged.size()) {
+  while (i < engine_rows.size()) {
     uint64_t dp = 0, sp = 0, dq = 0, sq = 0;
     size_t j = i + 1;
-    if (j < merged.size() && pitch_ok(merged[i], merged[j], &dp, &sp)) {
+    if (j < engine_rows.size() && pitch_ok(engine_rows[i], engine_rows[j], &dp, &sp)) {
       ++j;
-      while (j < merged.size() && pitch_ok(merged[j - 1], merged[j], &dq, &sq) && dq == dp && sq == sp) ++j;
+      while (j < engine_rows.size() && pitch_ok(engine_rows[j - 1], engine_rows[j], &dq, &sq) && dq == dp &&
+             sq == sp)
+        ++j;
     }
     if (j - i >= kMinRun) {
-      if (!submit_run(merged, i, j - i, dp, sp, kind, stream))
-        singles.insert(singles.end(), merged.begin() + i, merged.begin() + j);
+      if (!submit_run(engine_rows, i, j - i, dp, sp, kind, stream))
+        for (size_t k = i; k < j; ++k) submit_1d(engine_rows[k], kind, stream);
       i = j;
     } else {
-      singles.push_back(merged[i]);
+      submit_1d(engine_rows[i], kind, stream);
       ++i;
     }
   }
-  std::vector<PinnedRange> seen;
-  std::vector<Seg> kernel_rows;   // device-visible addresses on both sides
-  std::vector<size_t> kernel_src; // index into singles of each kernel row
-  for (size_t k = 0; k < singles.size(); ++k) {
-    const Seg &s = singles[k];
-    const uint64_t h = d2h ? s.dst : s.src;
-    const uint64_t dev = s.bytes < kEngineRowBytes ? mapped(h, s.bytes, seen) : 0;
-    if (dev == 0) {
-      submit_1d(s, kind, stream);
-      continue;
-    }
-    kernel_rows.push_back(d2h ? Seg{dev, s.src, s.bytes} : Seg{s.dst, dev, s.bytes});
-    kernel_src.push_back(k);
-  }
-  // one row alone gains nothing from a launch over a copy-engine copy
-  if (kernel_rows.size() == 1)
-    submit_1d(singles[kernel_src[0]], kind, stream);
-  else if (!kernel_rows.empty())
-    launch_rows(kernel_rows, stream);
 }
 
 void dma_copy_diagnose(const lmc_dma_segment *rows, int64_t n, bool d2h, hipStream_t stream, double *copy_us) {

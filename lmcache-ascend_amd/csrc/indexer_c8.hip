@@ -18,9 +18,11 @@
 // skipped, as in the reference kernel.
 //
 // Work mapping: grid (token tiles of the chunk capacity, chunk, layer); a
-// group of 16 lanes owns a token: up to 16 lanes move its key row in
+// group of lanes owns one or more tokens (8 lanes x 4 tokens when packing,
+// 16 lanes x 1 token when unpacking): the lanes move the key rows in
 // 16-byte accesses (bytewise when the packet is not 16-byte aligned) and
-// one lane its scale.  Every access is bounded by the checks above.
+// one lane per token its scale.  Every access is bounded by the checks
+// above.
 #include "common.h"
 
 #include <algorithm>
@@ -32,9 +34,14 @@ namespace lmc {
 namespace {
 
 constexpr int kC8Threads = 256;
-constexpr int kC8Group = 16;             // lanes per token
 constexpr int kC8Layers = 32;            // layers per launch (kernargs)
-constexpr int kC8Tokens = kC8Threads / kC8Group;
+// Lanes per token and tokens per lane group.  Packing reads the cache, and
+// a wave that keeps four tokens' rows in flight per lane moves 40% more
+// than one with a single token.  Unpacking reads the packet, often pinned
+// host memory, and the PCIe read path moves most with few tokens per wave
+// (measured on MI355X: 16 lanes x 1 token 53 GB/s, 8 x 1 48, 8 x 4 42).
+constexpr int kPackGroup = 8, kPackUnroll = 4;
+constexpr int kUnpackGroup = 16, kUnpackUnroll = 1;
 
 struct C8Layer {
   uint64_t keys;
@@ -65,46 +72,112 @@ __device__ __forceinline__ int64_t c8_index(const void *p, int is32, int64_t i) 
               : static_cast<const int64_t *>(p)[i];
 }
 
+// Grid (tiles of kC8Tokens tokens, chunks, layers).  A group of kC8Group
+// lanes owns kC8Unroll consecutive tokens of the tile.
+// Each lane issues every key load of the group's tokens (one or two 16-byte
+// accesses per token for 128- or 256-byte keys), then the stores; lane u of
+// the group moves token u's 2-byte scale.
+template <int kC8Group, int kC8Unroll>
 __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
+  using V = unsigned int __attribute__((ext_vector_type(4)));
+  constexpr int kKeyVecs = 256 / 16 / kC8Group;  // per lane, widest key row
+  constexpr int kC8Tokens = kC8Threads / kC8Group * kC8Unroll;
   const int64_t c = blockIdx.y;
   const int li = blockIdx.z;
   const C8Layer &L = job.layer[li];
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kC8Tokens + threadIdx.x / kC8Group;
+  const int grp = threadIdx.x / kC8Group;
   const int gl = threadIdx.x % kC8Group;
   const int64_t start = job.fixed ? c * job.capacity : c8_index(job.offsets, job.meta_i32, c);
   const int64_t remaining = job.slot_count - start;
   const int64_t count = job.fixed ? (remaining < job.capacity ? remaining : job.capacity)
                                   : c8_index(job.counts, job.meta_i32, c);
   const uint64_t packet = static_cast<uint64_t>(job.packets[li * job.chunks + c]);
-  if (!packet || count <= 0 || count > job.capacity || start < 0 ||
-      start > job.slot_count || count > job.slot_count - start || t >= count)
+  if (!packet || count <= 0 || count > job.capacity || start < 0 || start > job.slot_count ||
+      count > job.slot_count - start)
     return;
-  const int64_t slot = c8_index(job.slots, job.slot_i32, start + t);
-  if (slot < 0 || slot >= job.cache_slots) return;
-  const int64_t phys =
-      L.block_map
-          ? static_cast<int64_t>(reinterpret_cast<const int32_t *>(L.block_map)[slot / 128]) * 128 +
-                slot % 128
-          : slot + (slot / 128) * (L.slot_factor - 1) * 128;
-  if (phys < 0 || phys + 1 > job.cache_slots * L.slot_factor) return;
-  uint8_t *pk = reinterpret_cast<uint8_t *>(packet) + t * L.key_bytes;
-  uint8_t *ck = reinterpret_cast<uint8_t *>(L.keys) + phys * L.key_bytes;
-  uint8_t *dst = job.from_npu ? pk : ck;
-  const uint8_t *src = job.from_npu ? ck : pk;
-  if ((packet & 15) == 0) {
-    using V = unsigned int __attribute__((ext_vector_type(4)));
-    for (int v = gl; v < L.key_bytes / 16; v += kC8Group)
-      reinterpret_cast<V *>(dst)[v] = reinterpret_cast<const V *>(src)[v];
-  } else {
-    for (int b = gl; b < L.key_bytes; b += kC8Group) dst[b] = src[b];
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kC8Tokens + grp * kC8Unroll;
+  if (t0 >= count) return;
+  const int kb = L.key_bytes;
+  const bool vec = ((packet | L.keys) & 15) == 0;
+  const int nv = kb / 16;
+  V x[kC8Unroll][kKeyVecs];
+  // Unpacking reads the packet, whose rows do not depend on the slots:
+  // those loads go out before the slot lookups.
+  if (!job.from_npu && vec) {
+#pragma unroll
+    for (int u = 0; u < kC8Unroll; ++u) {
+      if (t0 + u >= count) continue;
+      const V *src = reinterpret_cast<const V *>(packet + (t0 + u) * kb);
+#pragma unroll
+      for (int k = 0; k < kKeyVecs; ++k)
+        if (gl + k * kC8Group < nv) x[u][k] = src[gl + k * kC8Group];
+    }
   }
-  if (L.scales && gl == 0) {
-    uint8_t *ps = reinterpret_cast<uint8_t *>(packet) + count * L.key_bytes + t * 2;
-    uint8_t *cs = reinterpret_cast<uint8_t *>(L.scales) + phys * 2;
-    uint8_t *d = job.from_npu ? ps : cs;
-    const uint8_t *s = job.from_npu ? cs : ps;
-    d[0] = s[0];
-    d[1] = s[1];
+  int64_t phys[kC8Unroll];
+#pragma unroll
+  for (int u = 0; u < kC8Unroll; ++u) {
+    const int64_t t = t0 + u;
+    phys[u] = -1;
+    if (t >= count) continue;
+    const int64_t slot = c8_index(job.slots, job.slot_i32, start + t);
+    if (slot < 0 || slot >= job.cache_slots) continue;
+    const int64_t p =
+        L.block_map
+            ? static_cast<int64_t>(reinterpret_cast<const int32_t *>(L.block_map)[slot / 128]) * 128 +
+                  slot % 128
+            : slot + (slot / 128) * (L.slot_factor - 1) * 128;
+    if (p >= 0 && p < job.cache_slots * L.slot_factor) phys[u] = p;
+  }
+  if (vec) {
+    if (job.from_npu) {
+#pragma unroll
+      for (int u = 0; u < kC8Unroll; ++u) {
+        if (phys[u] < 0) continue;
+        const V *src = reinterpret_cast<const V *>(L.keys + phys[u] * kb);
+#pragma unroll
+        for (int k = 0; k < kKeyVecs; ++k)
+          if (gl + k * kC8Group < nv) x[u][k] = src[gl + k * kC8Group];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kC8Unroll; ++u) {
+      if (phys[u] < 0) continue;
+      V *dst = reinterpret_cast<V *>(job.from_npu ? packet + (t0 + u) * kb : L.keys + phys[u] * kb);
+#pragma unroll
+      for (int k = 0; k < kKeyVecs; ++k)
+        if (gl + k * kC8Group < nv) dst[gl + k * kC8Group] = x[u][k];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kC8Unroll; ++u) {
+      if (phys[u] < 0) continue;
+      uint8_t *pk = reinterpret_cast<uint8_t *>(packet) + (t0 + u) * kb;
+      uint8_t *ck = reinterpret_cast<uint8_t *>(L.keys) + phys[u] * kb;
+      uint8_t *dst = job.from_npu ? pk : ck;
+      const uint8_t *src = job.from_npu ? ck : pk;
+      for (int b = gl; b < kb; b += kC8Group) dst[b] = src[b];
+    }
+  }
+  if (L.scales && gl < kC8Unroll) {
+    // lane gl moves the scale of token gl (unrolled selection keeps phys[]
+    // in registers)
+    int64_t ph = -1;
+#pragma unroll
+    for (int u = 0; u < kC8Unroll; ++u)
+      if (gl == u) ph = phys[u];
+    if (ph >= 0) {
+      const int64_t t = t0 + gl;
+      uint8_t *ps = reinterpret_cast<uint8_t *>(packet) + count * kb + t * 2;
+      uint8_t *cs = reinterpret_cast<uint8_t *>(L.scales) + ph * 2;
+      uint8_t *d = job.from_npu ? ps : cs;
+      const uint8_t *s = job.from_npu ? cs : ps;
+      if ((packet & 1) == 0) {
+        *reinterpret_cast<uint16_t *>(d) = *reinterpret_cast<const uint16_t *>(s);
+      } else {
+        d[0] = s[0];
+        d[1] = s[1];
+      }
+    }
   }
 }
 
@@ -209,7 +282,9 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
   job.capacity = capacity;
   job.slot_count = slot_count;
   job.cache_slots = cache_slots;
-  const int64_t tiles = (capacity + kC8Tokens - 1) / kC8Tokens;
+  const int64_t tile_tokens = from_npu ? kC8Threads / kPackGroup * kPackUnroll
+                                      : kC8Threads / kUnpackGroup * kUnpackUnroll;
+  const int64_t tiles = (capacity + tile_tokens - 1) / tile_tokens;
   check(tiles < (int64_t(1) << 31), "C8 transfer grid is too large");
   for (int l0 = 0; l0 < n_layers; l0 += kC8Layers) {
     const int nl = std::min(kC8Layers, n_layers - l0);
@@ -224,8 +299,12 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
       L.key_bytes = static_cast<int32_t>(128 * elem_size(k));
       L.slot_factor = static_cast<int32_t>(factors[l0 + i]);
     }
-    hipLaunchKernelGGL(indexer_c8_copy, dim3(static_cast<unsigned>(tiles), chunks, nl),
-                       dim3(kC8Threads), 0, stream, j);
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks), nl);
+    if (from_npu)
+      hipLaunchKernelGGL((indexer_c8_copy<kPackGroup, kPackUnroll>), grid, dim3(kC8Threads), 0, stream, j);
+    else
+      hipLaunchKernelGGL((indexer_c8_copy<kUnpackGroup, kUnpackUnroll>), grid, dim3(kC8Threads), 0, stream,
+                         j);
     hip_check(hipGetLastError(), "indexer_c8_copy launch");
   }
 }

@@ -48,6 +48,7 @@ namespace lmc {
 namespace {
 
 constexpr int kEntThreads = 256;
+constexpr int kEntUnroll = 4;  // accesses per lane and plane in one pass
 
 enum EntryMode : int32_t {
   kDenseFixed = 0,
@@ -224,18 +225,26 @@ __global__ void __launch_bounds__(kEntThreads) kv_entry_copy(EntryJob job) {
     return;
   }
   if (job.one_pass) {
-    // Every plane's row fits one pass of the group: all loads, then all
-    // stores.
-    V x[kMaxPlanes];
+    // Every plane's row fits kEntUnroll passes of the group: all loads,
+    // then all stores.
+    V x[kMaxPlanes][kEntUnroll];
 #pragma unroll
     for (int p = 0; p < kMaxPlanes; ++p)
-      if (p < job.n_planes && gl * VEC < job.plane[p].row_bytes)
-        x[p] = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + gl);
+#pragma unroll
+      for (int k = 0; k < kEntUnroll; ++k) {
+        const int v = gl + k * G;
+        if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes)
+          x[p][k] = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + v);
+      }
 #pragma unroll
     for (int p = 0; p < kMaxPlanes; ++p)
-      if (p < job.n_planes && gl * VEC < job.plane[p].row_bytes) {
-        st<V, NT>(reinterpret_cast<V *>(dst[p]) + gl, x[p]);
-        if (third) st<V, NT>(reinterpret_cast<V *>(mir[p]) + gl, x[p]);
+#pragma unroll
+      for (int k = 0; k < kEntUnroll; ++k) {
+        const int v = gl + k * G;
+        if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes) {
+          st<V, NT>(reinterpret_cast<V *>(dst[p]) + v, x[p][k]);
+          if (third) st<V, NT>(reinterpret_cast<V *>(mir[p]) + v, x[p][k]);
+        }
       }
     return;
   }
@@ -309,10 +318,17 @@ void launch_entries(EntryJob job, bool host_lmc, hipStream_t stream) {
   }
   const int vec = vec_for(gv);
   const int64_t vecs = std::max<int64_t>(1, widest / vec);
+  // Lanes per entry: enough for kEntUnroll accesses per lane to cover the
+  // widest row (up to a wave), so a wave holds several entries and each
+  // lane keeps several loads in flight.  Reads of host memory keep one
+  // access per lane, a whole row per wave instruction: the PCIe read path
+  // moves fewer bytes per second when each wave splits its reads over
+  // several rows.
+  const int unroll = host_lmc && !job.page2lmc ? 1 : kEntUnroll;
   int shift = 0;
-  while ((int64_t(1) << shift) < vecs && shift < 6) ++shift;
+  while ((int64_t(unroll) << shift) < vecs && shift < 6) ++shift;
   job.group_shift = shift;
-  job.one_pass = vecs <= (int64_t(1) << shift);
+  job.one_pass = vecs <= (int64_t(unroll) << shift);
   const int64_t threads = job.n_entries << shift;
   const int64_t blocks = (threads + kEntThreads - 1) / kEntThreads;
   check(blocks < (int64_t(1) << 31), "too many entries in one call");

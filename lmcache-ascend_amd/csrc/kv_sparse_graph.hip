@@ -14,9 +14,10 @@
 // device from this replay's counts and limits, and every bound is checked
 // before an address is formed.
 //
-// Work mapping: a group of G lanes (a power of two up to 64, covering the
-// wider of the two rows in 16-byte accesses) owns one entry; rows whose
-// source is not 16-byte aligned are copied bytewise.
+// Work mapping: a group of G lanes (a power of two up to 64, enough for
+// four 16-byte accesses per lane to cover the wider of the two rows) owns
+// one entry and issues both rows' loads before their stores; rows whose
+// source or destination is not 16-byte aligned are copied bytewise.
 #include "common.h"
 
 #include <algorithm>
@@ -27,6 +28,7 @@ namespace lmc {
 namespace {
 
 constexpr int kSfaThreads = 256;
+constexpr int kSfaUnroll = 4;  // 16-byte accesses per lane and row in one pass
 
 struct SfaJob {
   uint64_t k;
@@ -46,15 +48,17 @@ struct SfaJob {
   int32_t k_bytes;
   int32_t pe_bytes;
   int32_t group_shift;
+  int32_t one_pass;
   int64_t dest_slots;
 };
 
+using SfaVec = unsigned int __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ void sfa_row(uint8_t *dst, const uint8_t *src,
                                         int bytes, int gl, int G) {
-  using V = unsigned int __attribute__((ext_vector_type(4)));
-  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+  if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
     for (int v = gl; v < bytes / 16; v += G)
-      reinterpret_cast<V *>(dst)[v] = reinterpret_cast<const V *>(src)[v];
+      reinterpret_cast<SfaVec *>(dst)[v] = reinterpret_cast<const SfaVec *>(src)[v];
   } else {
     for (int b = gl; b < bytes; b += G) dst[b] = src[b];
   }
@@ -68,14 +72,16 @@ __global__ void __launch_bounds__(kSfaThreads) sfa_copy(SfaJob job) {
   if (e >= static_cast<int64_t>(job.requests) * job.row_width) return;
   const int r = static_cast<int>(e / job.row_width);
   const int col = static_cast<int>(e - static_cast<int64_t>(r) * job.row_width);
+  // The row's count and limit and the entry's token and slot are
+  // independent loads, issued together.
   const int32_t cnt = job.counts[static_cast<int64_t>(r) * job.count_stride];
   const int32_t lim = job.limits[r];
-  const int32_t active = (lim <= 0 || cnt <= 0) ? 0 : (cnt < job.row_width ? cnt : job.row_width);
-  if (col >= active) return;
   const int64_t token = job.sel_i64 ? static_cast<const int64_t *>(job.selected)[e]
                                     : static_cast<const int32_t *>(job.selected)[e];
   const int64_t dest = job.slot_i64 ? static_cast<const int64_t *>(job.slots)[e]
                                     : static_cast<const int32_t *>(job.slots)[e];
+  const int32_t active = (lim <= 0 || cnt <= 0) ? 0 : (cnt < job.row_width ? cnt : job.row_width);
+  if (col >= active) return;
   if (token < 0 || token >= lim || dest < 0 || dest >= job.dest_slots) return;
   const int64_t chunk = token / job.chunk_size;
   if (chunk >= job.chunks_per_request) return;
@@ -84,10 +90,33 @@ __global__ void __launch_bounds__(kSfaThreads) sfa_copy(SfaJob job) {
   const uint64_t ks = job.table[ti];
   const uint64_t ps = job.table[static_cast<int64_t>(job.requests) * job.chunks_per_request + ti];
   if (ks == 0 || ps == 0) return;
-  sfa_row(reinterpret_cast<uint8_t *>(job.k) + dest * job.k_bytes,
-          reinterpret_cast<const uint8_t *>(ks) + off * job.k_bytes, job.k_bytes, gl, G);
-  sfa_row(reinterpret_cast<uint8_t *>(job.pe) + dest * job.pe_bytes,
-          reinterpret_cast<const uint8_t *>(ps) + off * job.pe_bytes, job.pe_bytes, gl, G);
+  const uint8_t *ksrc = reinterpret_cast<const uint8_t *>(ks) + off * job.k_bytes;
+  const uint8_t *psrc = reinterpret_cast<const uint8_t *>(ps) + off * job.pe_bytes;
+  uint8_t *kdst = reinterpret_cast<uint8_t *>(job.k) + dest * job.k_bytes;
+  uint8_t *pdst = reinterpret_cast<uint8_t *>(job.pe) + dest * job.pe_bytes;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(ksrc) | reinterpret_cast<uintptr_t>(psrc) |
+                          reinterpret_cast<uintptr_t>(kdst) | reinterpret_cast<uintptr_t>(pdst);
+  if (job.one_pass && (align & 15) == 0) {
+    // Both rows fit kSfaUnroll passes of the group: all loads, then all
+    // stores.
+    const int kv = job.k_bytes / 16, pv = job.pe_bytes / 16;
+    SfaVec xk[kSfaUnroll], xp[kSfaUnroll];
+#pragma unroll
+    for (int u = 0; u < kSfaUnroll; ++u) {
+      const int v = gl + u * G;
+      if (v < kv) xk[u] = reinterpret_cast<const SfaVec *>(ksrc)[v];
+      if (v < pv) xp[u] = reinterpret_cast<const SfaVec *>(psrc)[v];
+    }
+#pragma unroll
+    for (int u = 0; u < kSfaUnroll; ++u) {
+      const int v = gl + u * G;
+      if (v < kv) reinterpret_cast<SfaVec *>(kdst)[v] = xk[u];
+      if (v < pv) reinterpret_cast<SfaVec *>(pdst)[v] = xp[u];
+    }
+    return;
+  }
+  sfa_row(kdst, ksrc, job.k_bytes, gl, G);
+  sfa_row(pdst, psrc, job.pe_bytes, gl, G);
 }
 
 bool contiguous(const lmc_tensor &t) {
@@ -160,10 +189,14 @@ void sparse_graph(const lmc_tensor &k, const lmc_tensor &pe, int64_t kH, int64_t
   job.k_bytes = static_cast<int32_t>(k_bytes);
   job.pe_bytes = static_cast<int32_t>(pe_bytes);
   job.dest_slots = std::min(nbytes(k) / k_bytes, nbytes(pe) / pe_bytes);
+  // Lanes per entry: enough for kSfaUnroll accesses per lane to cover the
+  // wider row (up to a wave), so a wave holds several entries and each lane
+  // keeps several loads in flight.
   const int64_t vecs = std::max(k_bytes, pe_bytes) / 16;
   int shift = 0;
-  while ((int64_t(1) << shift) < vecs && shift < 6) ++shift;
+  while ((int64_t(kSfaUnroll) << shift) < vecs && shift < 6) ++shift;
   job.group_shift = shift;
+  job.one_pass = vecs <= (int64_t(kSfaUnroll) << shift);
   const int64_t threads = numel(sel) << shift;
   const int64_t blocks = (threads + kSfaThreads - 1) / kSfaThreads;
   // max_aiv_cores caps the reference's AI-vector cores for prefetch callers;

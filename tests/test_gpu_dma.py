@@ -109,13 +109,15 @@ def test_random_disjoint_rows(ops, align, d2h):
     assert np.array_equal(_np(dev), spaces[1][1])
 
 
+@pytest.mark.parametrize("pinned", [True, False])
 @pytest.mark.parametrize("d2h", [False, True])
-def test_merge_and_rectangular_runs(ops, d2h):
+def test_merge_and_rectangular_runs(ops, d2h, pinned):
     """Rows adjacent on both sides (merged), equal-pitch runs (one
-    rectangular copy), a pitch smaller than the row on the source side
-    (overlapping sources: one copy per row) and a broadcast source."""
+    rectangular copy when the host side is pageable, the copy kernel when it
+    is pinned), a pitch smaller than the row on the source side (overlapping
+    sources: one copy per row) and a broadcast source."""
     gen = torch.Generator().manual_seed(11 + d2h)
-    host = _rand_u8(1 << 18, gen)
+    host = _rand_u8(1 << 18, gen, pinned)
     dev = torch.randint(0, 256, (1 << 18,), dtype=torch.uint8, generator=gen).to(DEV)
     h, d = host.data_ptr(), dev.data_ptr()
     rows = []
@@ -140,18 +142,26 @@ def test_merge_and_rectangular_runs(ops, d2h):
 
 @pytest.mark.parametrize("d2h", [False, True])
 def test_run_across_two_allocations(ops, d2h):
-    """Two rows at constant pitches whose device side lies in two separate
-    allocations: the runtime refuses one rectangle over both, and the rows
-    still land."""
+    """Four rows at constant pitches over pageable host memory whose device
+    side lies in two separate allocations: the runtime refuses one rectangle
+    over them, and the rows still land."""
     gen = torch.Generator().manual_seed(21 + d2h)
-    host = _rand_u8(1 << 20, gen)
-    a = torch.randint(0, 256, (24 << 20,), dtype=torch.uint8, generator=gen).to(DEV)
-    b = torch.randint(0, 256, (24 << 20,), dtype=torch.uint8, generator=gen).to(DEV)
+    host = _rand_u8(1 << 20, gen, pinned=False)
+    size = 64 << 20
+    a = torch.randint(0, 256, (size,), dtype=torch.uint8, generator=gen).to(DEV)
+    b = torch.randint(0, 256, (size,), dtype=torch.uint8, generator=gen).to(DEV)
     lo, hi = sorted([a, b], key=lambda t: t.data_ptr())
-    n = 4096
+    n, a = 4096, 1000
     h = host.data_ptr()
-    dev_rows = [lo.data_ptr() + 1000, hi.data_ptr() + 1000]
-    host_rows = [h + 0, h + 8192]
+    gap = hi.data_ptr() - lo.data_ptr()
+    pitch = (gap + 1) // 2                 # rows 0-1 in `lo`, rows 2-3 in `hi`
+    offs = [a + k * pitch for k in range(4)]
+    dev_rows = [lo.data_ptr() + o if o + n <= size else hi.data_ptr() + o - gap for o in offs]
+    inside = [lo.data_ptr() <= r and r + n <= lo.data_ptr() + size or
+              hi.data_ptr() <= r and r + n <= hi.data_ptr() + size for r in dev_rows]
+    if not all(inside) or pitch < n:
+        pytest.skip(f"the allocations are {gap} bytes apart: too far for one run over both")
+    host_rows = [h + 8192 * k for k in range(4)]
     rows = [(hr, dr, n) if d2h else (dr, hr, n) for dr, hr in zip(dev_rows, host_rows)]
     spaces = _spaces(host, [lo, hi])
     ok.layerwise_dma_copy(spaces, rows)
