@@ -123,6 +123,60 @@ def cpu_baseline(budget_s=10.0):
     }
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_torch_path(torch, budget_s=3.0):
+    """The reference's CPU-style path (tools/cpu_vllm_runtime.py:352-419:
+    index_select for the store, index_copy_ for the retrieve, per layer and
+    plane) on the same 16 chunks x 32 layers x 2 planes x 2 KiB rows
+    against a 64-block-per-layer host pool, with every thread torch may use
+    and with one thread."""
+    g = torch.Generator().manual_seed(0)
+    nb_cpu = 64
+    pool = [[torch.randn((nb_cpu * BS, W), generator=g).to(torch.bfloat16) for _ in range(2)] for _ in range(L)]
+    blocks = [int(b) for b in torch.randperm(nb_cpu, generator=g)[:33]]
+    slots = torch.tensor(block_slots(blocks, BS, REQUEST_LENGTHS), dtype=torch.int64)
+    n_chunks = len(slots) // CHUNK
+    lmc = [torch.empty((2, L, CHUNK, W), dtype=torch.bfloat16) for _ in range(n_chunks)]
+
+    def one_pass():
+        for i in range(n_chunks):
+            s = slots[i * CHUNK:(i + 1) * CHUNK]
+            for l in range(L):
+                for p in range(2):
+                    torch.index_select(pool[l][p], 0, s, out=lmc[i][p, l])
+            for l in range(L):
+                for p in range(2):
+                    pool[l][p].index_copy_(0, s, lmc[i][p, l])
+        return 2 * 2 * L * len(slots) * W * ES
+
+    threads_all = torch.get_num_threads()
+    out = {"cpu_model": cpu_model(), "unit": "GB/s", "sample": "store+retrieve of 16 chunks [2,32,256,1024] bf16 "
+           "against a 64-block/layer host pool, torch index_select / index_copy_"}
+    for n in (threads_all, 1):
+        torch.set_num_threads(n)
+        one_pass()
+        payload, t0 = 0, time.perf_counter()
+        while True:
+            payload += one_pass()
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        dt = time.perf_counter() - t0
+        out[f"threads_{n}"] = {"value": round(payload / dt / 1e9, 3),
+                               "tokens_per_s": round(payload / (2 * 2 * L * W * ES) / dt)}
+    torch.set_num_threads(threads_all)
+    return out
+
+
 def load_traffic():
     """HBM traffic per launch from the committed rocprofv3 --pmc summary."""
     path = os.path.join(REPO, "profiles", "kv_rows_copy_llama8b_4096tok_traffic.json")
@@ -732,6 +786,7 @@ def main(argv=None):
     }
     if not args.skip_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        out["cpu_reference_style_path"] = cpu_torch_path(torch)
     print(json.dumps(out))
     return 0
 
