@@ -249,6 +249,198 @@ __global__ void __launch_bounds__(kEncLanes)
   lens[stream] = static_cast<int32_t>(wpos + ((nbits + 7) >> 3));
 }
 
+// Wave encode (T <= 256): 64 streams per block, four waves; a wave encodes
+// one whole stream at a time, so no lane walks a serial chain of symbols.
+//   1. The block's CDF rows and symbols are staged into LDS with coalesced
+//      loads, all issued before any LDS store; the symbols are transposed
+//      to one row per stream (an odd number of words per row).
+//   2. Per stream, lane s builds symbol s's (code, length) from the staged
+//      row (the wrap of rule L2 found with a ballot), and lane j takes the
+//      stream's tokens 4j .. 4j + 3 with one LDS read and looks their codes
+//      up with cross-lane shuffles.
+//   3. The lane's four codes become one run of at most 64 bits; an
+//      exclusive prefix sum over the wave gives the run's bit offset, and
+//      the run is ORed into the (at most three) words it touches of the
+//      wave's LDS bit buffer.
+//   4. Lane k stores word k of the row: one coalesced store per 256 bytes,
+//      and only bytes below min(chunk, stream length), as the single-lane
+//      encoder writes them.
+constexpr int kEncWaves = 4;
+constexpr int kEncTileThreads = kEncLanes * kEncWaves;
+constexpr int kEncTileMaxT = 4 * kEncLanes;
+
+__device__ __forceinline__ void put_word(uint8_t *row, int64_t chunk, uint32_t idx, uint32_t word,
+                                         int n, int word_stores) {
+  const int64_t at = static_cast<int64_t>(idx) * 4;
+  if (n == 4 && word_stores && at + 4 <= chunk)
+    *reinterpret_cast<uint32_t *>(row + at) = __builtin_bswap32(word);
+  else
+    put_bytes(row, chunk, at, word, n);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts
+// by 1, 2, 4 and 8 within each row of 16 lanes, then the last lane of row
+// 0 (row_bcast:15) and of row 1 (row_bcast:31) added to the rows after it.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  int x = static_cast<int>(v);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false); // row_bcast:15 to rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false); // row_bcast:31 to rows 2, 3
+  return static_cast<uint32_t>(x);
+}
+
+__global__ void __launch_bounds__(kEncTileThreads)
+    encode_wave_kernel(const int16_t *__restrict__ cdf,
+                       const uint8_t *__restrict__ in, int T, int C, int nb,
+                       uint8_t *__restrict__ out, int64_t chunk,
+                       int32_t *__restrict__ lens, int tiles, int word_stores, int vec_tile,
+                       int sym_stride, int cap_words) {
+  // [64][nb + 1] int16 rows | [64][sym_stride] u32 symbols | [4][2][cap_words] u32 bits
+  extern __shared__ uint32_t lds[];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wv = tid / kEncLanes;
+  const int lane = tid % kEncLanes;
+  const int l = blockIdx.x / tiles;
+  const int c0 = (blockIdx.x % tiles) * kEncLanes;
+  const int cnt = C - c0 < kEncLanes ? C - c0 : kEncLanes;
+  const int64_t s0 = static_cast<int64_t>(l) * C + c0;
+  int16_t *stage = reinterpret_cast<int16_t *>(lds);
+  const int rows_words = ((nb + 1) * kEncLanes * 2 + 15) / 16 * 4;
+  uint8_t *tile = reinterpret_cast<uint8_t *>(lds + rows_words);
+  uint32_t *bitbuf = lds + rows_words + kEncLanes * sym_stride + 2 * wv * cap_words;
+
+  // 1. Rows and symbols: every load of the thread, then the LDS stores.
+  {
+    const int16_t *rsrc = cdf + s0 * (nb + 1);
+    const int rcount = cnt * (nb + 1);
+    constexpr int kR = 4;
+    int16_t rv[kR];
+    int ri[kR];
+#pragma unroll
+    for (int k = 0; k < kR; ++k) {
+      const int i = k * kEncTileThreads + tid;
+      ri[k] = i < rcount ? i : rcount - 1;
+      rv[k] = rsrc[ri[k]];
+    }
+    const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
+    const int pieces = T * 4;
+    const int row_bytes = sym_stride * 4;
+    if (vec_tile && cnt == kEncLanes) {
+      uint4 v[4];
+      int pi[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = k * kEncTileThreads + tid;
+        pi[k] = i < pieces ? i : pieces - 1;
+        v[k] = *reinterpret_cast<const uint4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint8_t *d = tile + (pi[k] & 3) * 16 * row_bytes + (pi[k] >> 2);
+        const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) d[j * row_bytes] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
+      }
+    } else {
+      for (int i = tid; i < T * kEncLanes; i += kEncTileThreads) {
+        const int c = i % kEncLanes, t = i / kEncLanes;
+        tile[c * row_bytes + t] = c < cnt ? src[static_cast<int64_t>(t) * C + c] : 0;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kR; ++k) stage[ri[k]] = rv[k];
+    for (int i = kR * kEncTileThreads + tid; i < rcount; i += kEncTileThreads) stage[i] = rsrc[i];
+  }
+  __syncthreads();
+
+  // Two streams per step (st and st + kEncWaves), so their LDS round trips
+  // overlap.
+  for (int st0 = wv; st0 < cnt; st0 += 2 * kEncWaves) {
+    int stv[2];
+    bool on[2];
+    int entry[2];
+    uint32_t word[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      stv[j] = st0 + j * kEncWaves;
+      on[j] = stv[j] < cnt;
+      // 2. Code table: lane s holds symbol s's (code << 5) | length.
+      const int16_t *row = stage + (on[j] ? stv[j] : st0) * (nb + 1);
+      const uint32_t raw = lane < nb ? static_cast<uint16_t>(row[lane]) : 0u;
+      const uint32_t raw_n = lane + 1 < nb ? static_cast<uint16_t>(row[lane + 1]) : 0u;
+      const bool dec = lane + 1 < nb && (raw_n & 0xFFF0u) < (raw & 0xFFF0u);
+      const uint64_t decs = __ballot(dec);
+      const int wrap = decs ? __builtin_ctzll(decs) + 1 : nb;  // bases from here on are 0x10000
+      const uint32_t base = lane < wrap ? (raw & 0xFFF0u) : 0x10000u;
+      const uint32_t next = lane + 1 < wrap ? (raw_n & 0xFFF0u) : 0x10000u;
+      uint32_t len = raw & 0xFu;
+      if (len == 0 && next != base) len = kPrec - (31 - __builtin_clz(next - base));
+      const uint32_t code = len ? (base >> (kPrec - len)) & ((1u << len) - 1u) : 0u;
+      entry[j] = lane < nb ? static_cast<int>((code << 5) | len) : 0;
+      // Tokens 4 * lane .. + 3.
+      word[j] = (on[j] && 4 * lane < T)
+                    ? reinterpret_cast<const uint32_t *>(tile)[stv[j] * sym_stride + lane] : 0u;
+    }
+    uint64_t run[2];
+    uint32_t run_bits[2], pos[2], total[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      run[j] = 0;
+      run_bits[j] = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t v = (word[j] >> (8 * b)) & 0xFFu;
+        const uint32_t e = static_cast<uint32_t>(__shfl(entry[j], static_cast<int>(v & 63u)));
+        const bool ok = on[j] && 4 * lane + b < T && v < static_cast<uint32_t>(nb);
+        const uint32_t n = ok ? (e & 31u) : 0u;
+        run[j] = (run[j] << n) | (ok ? (e >> 5) : 0u);
+        run_bits[j] += n;
+      }
+    }
+    // 3. Exclusive prefix sums of the runs' lengths.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t incl = wave_incl_scan(run_bits[j]);
+      pos[j] = incl - run_bits[j];
+      total[j] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kEncLanes - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      for (int k = lane; k < cap_words; k += kEncLanes) bitbuf[j * cap_words + k] = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!run_bits[j]) continue;
+      uint32_t *bb = bitbuf + j * cap_words;
+      const uint64_t a = run[j] << (64 - run_bits[j]);  // top-aligned
+      const uint32_t hi = static_cast<uint32_t>(a >> 32), lo = static_cast<uint32_t>(a);
+      const uint32_t w0 = pos[j] >> 5, sh = pos[j] & 31u;
+      if (w0 < static_cast<uint32_t>(cap_words)) atomicOr(&bb[w0], hi >> sh);
+      if (sh + run_bits[j] > 32 && w0 + 1 < static_cast<uint32_t>(cap_words))
+        atomicOr(&bb[w0 + 1], sh ? (hi << (32 - sh)) | (lo >> sh) : lo);
+      if (sh + run_bits[j] > 64 && w0 + 2 < static_cast<uint32_t>(cap_words))
+        atomicOr(&bb[w0 + 2], lo << (32 - sh));
+    }
+    // 4. The rows.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!on[j]) continue;
+      const int64_t tbytes = (total[j] + 7) >> 3;
+      int64_t nbytes = tbytes < chunk ? tbytes : chunk;
+      nbytes = nbytes < 4 * static_cast<int64_t>(cap_words) ? nbytes : 4 * static_cast<int64_t>(cap_words);
+      uint8_t *orow = out + (s0 + stv[j]) * chunk;
+      for (int k = lane; static_cast<int64_t>(k) * 4 < nbytes; k += kEncLanes) {
+        const int64_t left = nbytes - 4 * static_cast<int64_t>(k);
+        put_word(orow, chunk, static_cast<uint32_t>(k), bitbuf[j * cap_words + k],
+                 left >= 4 ? 4 : static_cast<int>(left), word_stores);
+      }
+      if (lane == 0) lens[s0 + stv[j]] = static_cast<int32_t>(tbytes);
+    }
+  }
+}
+
 // Decode: 64 streams per block (one wave) and 40 KiB of LDS per block, so
 // the four blocks of a CU's four SIMDs fit its 160 KiB.  The block's 64
 // streams are adjacent in the byte buffer; their CDF rows and (up to the
@@ -696,10 +888,31 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
     if (L == 0 || C == 0) return;
     DeviceGuard guard(in.device);
     const int tiles = static_cast<int>((C + kEncLanes - 1) / kEncLanes);
-    const size_t lds = static_cast<size_t>(nb) * kEncLanes * 4 +
-                       static_cast<size_t>(nb + 1) * kEncLanes * 2;
     const int word_stores =
         (chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(ob.data) & 3) == 0) ? 1 : 0;
+    if (T > 0 && T <= kEncTileMaxT && nb <= kEncLanes) {
+      // Bits past min(chunk, 2 bytes per symbol) are never written (codes
+      // are at most 16 bits), so a wave's bit buffer holds that many bytes.
+      const int64_t cap_bytes = std::min<int64_t>(chunk, 2 * T);
+      const int cap_words = static_cast<int>((cap_bytes + 3) / 4);
+      const int sym_stride = (((T + 3) / 4) + 1) | 1;
+      const size_t lds = 4 * ((static_cast<size_t>(nb + 1) * kEncLanes * 2 + 15) / 16 * 4 +
+                              static_cast<size_t>(kEncLanes) * sym_stride +
+                              static_cast<size_t>(2 * kEncWaves) * cap_words);
+      const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
+      check(lds <= 65536, "encode: LDS budget exceeded");
+      hipLaunchKernelGGL(encode_wave_kernel, dim3(L * tiles), dim3(kEncTileThreads), lds,
+                         static_cast<hipStream_t>(stream),
+                         static_cast<const int16_t *>(cdf.data),
+                         static_cast<const uint8_t *>(in.data), (int)T, (int)C,
+                         (int)nb, static_cast<uint8_t *>(ob.data), chunk,
+                         static_cast<int32_t *>(ol.data), tiles, word_stores, vec_tile, sym_stride,
+                         cap_words);
+      hip_check(hipGetLastError(), "encode_wave_kernel launch");
+      return;
+    }
+    const size_t lds = static_cast<size_t>(nb) * kEncLanes * 4 +
+                       static_cast<size_t>(nb + 1) * kEncLanes * 2;
     hipLaunchKernelGGL(encode_kernel, dim3(L * tiles), dim3(kEncLanes), lds,
                        static_cast<hipStream_t>(stream),
                        static_cast<const int16_t *>(cdf.data),
