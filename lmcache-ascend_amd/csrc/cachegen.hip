@@ -172,6 +172,149 @@ __global__ void __launch_bounds__(kLanes)
   o[nb] = 0;
 }
 
+// Tiled calculate_cdf (1 <= T <= 256): 64 streams per block, four waves.
+// The block's symbols [T][64] are staged into LDS with 16-byte loads; wave
+// q counts the q-th quarter of the tokens into per-stream LDS histogram
+// columns (no-return adds, one column per lane); wave 0 then derives each
+// stream's CDF by rule L4, with closed forms for the Shannon length (the
+// smallest l with count << l >= n) and for the aligned width (the interval
+// width capped by the lowest set bit of the running base),
+// and the block's 64 rows, contiguous in the output, leave as coalesced
+// dword stores.  Rows equal the single-lane kernel's.
+constexpr int kCdfWaves = 4;
+constexpr int kCdfThreads = 64 * kCdfWaves;
+constexpr int kCdfMaxT = 256;
+
+template <int kBins>  // register capacity for code lengths: nb <= kBins
+__global__ void __launch_bounds__(kCdfThreads)
+    cdf_tile_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
+                    int16_t *__restrict__ out, int tiles, int vec_tile) {
+  // [T][64] u8 symbols | [nb][64] u32 histogram | [64][nb + 1] int16 rows
+  extern __shared__ uint32_t lds[];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int q = tid / 64;
+  const int lane = tid % 64;
+  const int l = blockIdx.x / tiles;
+  const int c0 = (blockIdx.x % tiles) * 64;
+  const int cnt = C - c0 < 64 ? C - c0 : 64;
+  uint8_t *tile = reinterpret_cast<uint8_t *>(lds);
+  const int tile_words = (T * 64 + 15) / 16 * 4;
+  uint32_t *hist = lds + tile_words;
+  int16_t *rows = reinterpret_cast<int16_t *>(hist + nb * 64);
+  for (int i = tid; i < nb * 64; i += kCdfThreads) hist[i] = 0;
+  const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
+  const int pieces = T * 4;
+  if (vec_tile && cnt == 64) {
+    uint4 v[4];
+    int pi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = k * kCdfThreads + tid;
+      pi[k] = i < pieces ? i : pieces - 1;
+      v[k] = *reinterpret_cast<const uint4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) reinterpret_cast<uint4 *>(tile)[pi[k]] = v[k];
+  } else {
+    for (int i = tid; i < T * 64; i += kCdfThreads) {
+      const int c = i % 64;
+      tile[i] = c < cnt ? src[static_cast<int64_t>(i / 64) * C + c] : 0xFFu;
+    }
+  }
+  __syncthreads();
+  const int Tq = (T + kCdfWaves - 1) / kCdfWaves;
+  const int tb = q * Tq < T ? q * Tq : T;
+  const int te = tb + Tq < T ? tb + Tq : T;
+  if (lane < cnt) {
+    for (int t0 = tb; t0 < te; t0 += kBatch) {
+      uint32_t sym[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) sym[i] = t0 + i < te ? tile[(t0 + i) * 64 + lane] : 0xFFu;
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        if (sym[i] < static_cast<uint32_t>(nb)) atomicAdd(&hist[sym[i] * 64 + lane], 1u);
+    }
+  }
+  __syncthreads();
+  if (q == 0 && lane < cnt) {
+    const uint32_t *col = hist + lane;
+    uint32_t n = 0;
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) n += s < nb ? col[s * 64] : 0u;
+    uint32_t len[kBins];
+    uint32_t kraft = 0;  // units of 2^-16
+    const int ln = 31 - __builtin_clz(n | 1u);
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) {
+      const uint32_t cs = s < nb ? col[s * 64] : 0u;
+      uint32_t x = 0;
+      if (cs) {
+        x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs)));
+        if ((static_cast<uint64_t>(cs) << x) < n) ++x;
+        x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
+        kraft += 1u << (kPrec - x);
+      }
+      len[s] = x;
+    }
+    // Kraft repair: lengthen the rarest present symbol below the cap (the
+    // last one among equals) until the code fits.
+    while (kraft > (1u << kPrec)) {
+      int pick = -1;
+      uint32_t best = 0;
+#pragma unroll
+      for (int s = 0; s < kBins; ++s) {
+        const uint32_t cs = s < nb ? col[s * 64] : 0u;
+        if (len[s] != 0 && len[s] < kMaxLen && (pick < 0 || cs <= best)) {
+          pick = s;
+          best = cs;
+        }
+      }
+      if (pick < 0) break;
+#pragma unroll
+      for (int s = 0; s < kBins; ++s)
+        if (s == pick) {
+          kraft -= 1u << (kPrec - len[s] - 1);
+          ++len[s];
+        }
+    }
+    // Aligned in-order assignment.  A symbol's base is the running position
+    // `pos`; an absent symbol (length 0) gets the same value, which is the
+    // base of the next present symbol (or the end).
+    int16_t *row = rows + lane * (nb + 1);
+    uint32_t pos = 0;
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) {
+      if (s < nb) {
+        uint32_t x = len[s];
+        if (x) {
+          uint32_t w = 1u << (kPrec - x);
+          const uint32_t low = pos & (0u - pos);  // lowest set bit (0 when pos == 0)
+          if (low && low < w) {
+            x += (31 - __builtin_clz(w)) - (31 - __builtin_clz(low));
+            w = low;
+          }
+          row[s] = static_cast<int16_t>(static_cast<uint16_t>((pos | x) & 0xFFFFu));
+          pos += w;
+        } else {
+          row[s] = static_cast<int16_t>(static_cast<uint16_t>(pos & 0xFFFFu));
+        }
+      }
+    }
+    row[nb] = 0;
+  }
+  __syncthreads();
+  // The block's rows are contiguous in the output.
+  int16_t *dst = out + (static_cast<int64_t>(l) * C + c0) * (nb + 1);
+  const int total = cnt * (nb + 1);
+  if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+    for (int i = tid; i < total / 2; i += kCdfThreads)
+      reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(rows)[i];
+    if ((total & 1) && tid == 0) dst[total - 1] = rows[total - 1];
+  } else {
+    for (int i = tid; i < total; i += kCdfThreads) dst[i] = rows[i];
+  }
+}
+
 __device__ __forceinline__ void put_bytes(uint8_t *row, int64_t chunk,
                                           int64_t at, uint32_t word, int n) {
   // `n` most significant bytes of `word` at byte offset `at`.
@@ -847,6 +990,24 @@ int lmc_calculate_cdf(const lmc_tensor *input, int32_t n_bins,
     check(T < (int64_t(1) << 26) && C < (int64_t(1) << 30), "input too large");
     if (L == 0 || C == 0) return;
     DeviceGuard guard(in.device);
+    if (T >= 1 && T <= kCdfMaxT) {
+      const int tiles64 = static_cast<int>((C + 63) / 64);
+      const size_t lds = 4 * (static_cast<size_t>((T * 64 + 15) / 16 * 4) + static_cast<size_t>(n_bins) * 64) +
+                         static_cast<size_t>(64) * (n_bins + 1) * 2;
+      const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
+      if (n_bins <= 32)
+        hipLaunchKernelGGL(cdf_tile_kernel<32>, dim3(L * tiles64), dim3(kCdfThreads), lds,
+                           static_cast<hipStream_t>(stream),
+                           static_cast<const uint8_t *>(in.data), (int)T, (int)C,
+                           n_bins, static_cast<int16_t *>(o.data), tiles64, vec_tile);
+      else
+        hipLaunchKernelGGL(cdf_tile_kernel<kMaxBins>, dim3(L * tiles64), dim3(kCdfThreads), lds,
+                           static_cast<hipStream_t>(stream),
+                           static_cast<const uint8_t *>(in.data), (int)T, (int)C,
+                           n_bins, static_cast<int16_t *>(o.data), tiles64, vec_tile);
+      hip_check(hipGetLastError(), "cdf_tile_kernel launch");
+      return;
+    }
     const int tiles = static_cast<int>((C + kLanes - 1) / kLanes);
     const size_t lds = static_cast<size_t>(n_bins) * kLanes * 4;
     hipLaunchKernelGGL(cdf_kernel, dim3(L * tiles), dim3(kLanes), lds,
