@@ -155,9 +155,13 @@ def test_encode_into_decode(ops, n_tokens, n_layers, num_heads):
     assert torch.equal(dec, d)
 
 
-def test_edge_cases_vs_oracle(ops):
-    rng = np.random.default_rng(5)
-    L, T, C, nb = 3, 300, 96, 16
+@pytest.mark.parametrize("T,C", [(300, 96), (256, 96), (255, 64), (256, 128), (97, 100), (1, 64)])
+def test_edge_cases_vs_oracle(ops, T, C):
+    """Tokens above 256 take the one-lane-per-stream kernels, 256 and below
+    the tiled ones; C = 96 leaves a partial block of 32 streams, C = 100 is
+    not a multiple of 16 (byte staging)."""
+    rng = np.random.default_rng(5 + T + C)
+    L, nb = 3, 16
     syms = rng.integers(0, nb, size=(L, T, C)).astype(np.uint8)
     syms[0, :, :5] = 7                    # constant channels: one 1-bit code
     syms[1, :, 10:20] = nb + 1            # out-of-range: not counted, not coded
@@ -176,7 +180,15 @@ def test_edge_cases_vs_oracle(ops):
     torch.cuda.synchronize()
     assert np.array_equal(lens.cpu().numpy(), want_len)
     assert np.array_equal(out.cpu().numpy(), want_out)
-    assert want_len.max() > chunk
+    if T >= 255:
+        assert want_len.max() > chunk
+    # round trip through the decoder where every stream fit its row
+    if want_len.max() <= chunk and C % 32 == 0:
+        stream, pref = oc.concat_streams(want_out, want_len)
+        dec = torch.zeros_like(d)
+        ops.decode_fast_prefsum(cdf, torch.from_numpy(stream).to(DEV), torch.from_numpy(pref).to(DEV), dec)
+        torch.cuda.synchronize()
+        assert np.array_equal(dec.cpu().numpy(), oc.decode(want_cdf, stream, pref, T))
 
 
 def test_single_bin_and_single_token(ops):
