@@ -19,10 +19,10 @@
 //
 // Work mapping: grid (token tiles of the chunk capacity, chunk, layer); a
 // group of lanes owns one or more tokens (8 lanes x 4 tokens when packing,
-// 16 lanes x 1 token when unpacking): the lanes move the key rows in
-// 16-byte accesses (bytewise when the packet is not 16-byte aligned) and
-// one lane per token its scale.  Every access is bounded by the checks
-// above.
+// 16 lanes x 4 tokens when unpacking), and the groups of a wave take
+// consecutive tokens: the lanes move the key rows in 16-byte accesses
+// (bytewise when the packet is not 16-byte aligned) and one lane per token
+// its scale.  Every access is bounded by the checks above.
 #include "common.h"
 
 #include <algorithm>
@@ -35,13 +35,16 @@ namespace {
 
 constexpr int kC8Threads = 256;
 constexpr int kC8Layers = 32;            // layers per launch (kernargs)
-// Lanes per token and tokens per lane group.  Packing reads the cache, and
-// a wave that keeps four tokens' rows in flight per lane moves 40% more
-// than one with a single token.  Unpacking reads the packet, often pinned
-// host memory, and the PCIe read path moves most with few tokens per wave
-// (measured on MI355X: 16 lanes x 1 token 53 GB/s, 8 x 1 48, 8 x 4 42).
+// Lanes per token and tokens per lane group.  Packing reads the cache and
+// keeps four tokens' rows in flight per lane.  Unpacking reads the packet,
+// usually pinned host memory, and the PCIe read path moves most with 512
+// bytes per wave access (16 lanes per token, half of them idle for 128-byte
+// int8 keys).  Measured on MI355X, 8 layers x 16 x 1024 int8 tokens:
+// unpacking pinned packets 16 x 4 55.5 GB/s, 16 x 1 53.5, 8 x 4 46.7;
+// device packets 12.8, 14.3 and 10.3 us.  Packing pinned packets 8 x 4
+// 54.6 GB/s.
 constexpr int kPackGroup = 8, kPackUnroll = 4;
-constexpr int kUnpackGroup = 16, kUnpackUnroll = 1;
+constexpr int kUnpackGroup = 16, kUnpackUnroll = 4;
 
 struct C8Layer {
   uint64_t keys;
@@ -73,8 +76,8 @@ __device__ __forceinline__ int64_t c8_index(const void *p, int is32, int64_t i) 
 }
 
 // Grid (tiles of kC8Tokens tokens, chunks, layers).  A group of kC8Group
-// lanes owns kC8Unroll consecutive tokens of the tile.
-// Each lane issues every key load of the group's tokens (one or two 16-byte
+// lanes owns kC8Unroll tokens of the tile, 64 / kC8Group apart; a wave owns
+// 64 / kC8Group x kC8Unroll consecutive tokens.  Each lane issues every key load of the group's tokens (one or two 16-byte
 // accesses per token for 128- or 256-byte keys), then the stores; lane u of
 // the group moves token u's 2-byte scale.
 template <int kC8Group, int kC8Unroll>
@@ -85,8 +88,10 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   const int64_t c = blockIdx.y;
   const int li = blockIdx.z;
   const C8Layer &L = job.layer[li];
-  const int grp = threadIdx.x / kC8Group;
+  constexpr int kGroupsPerWave = 64 / kC8Group;
   const int gl = threadIdx.x % kC8Group;
+  const int gw = (threadIdx.x & 63) / kC8Group;
+  const int wave = threadIdx.x >> 6;
   const int64_t start = job.fixed ? c * job.capacity : c8_index(job.offsets, job.meta_i32, c);
   const int64_t remaining = job.slot_count - start;
   const int64_t count = job.fixed ? (remaining < job.capacity ? remaining : job.capacity)
@@ -95,7 +100,12 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   if (!packet || count <= 0 || count > job.capacity || start < 0 || start > job.slot_count ||
       count > job.slot_count - start)
     return;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kC8Tokens + grp * kC8Unroll;
+  // Token u of this group: the wave's groups take consecutive tokens, so
+  // one access instruction of the wave covers kGroupsPerWave consecutive
+  // packet rows.
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kC8Tokens +
+                     wave * (kGroupsPerWave * kC8Unroll) + gw;
+  const auto tok = [&](int u) { return t0 + static_cast<int64_t>(u) * kGroupsPerWave; };
   if (t0 >= count) return;
   const int kb = L.key_bytes;
   const bool vec = ((packet | L.keys) & 15) == 0;
@@ -106,8 +116,8 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   if (!job.from_npu && vec) {
 #pragma unroll
     for (int u = 0; u < kC8Unroll; ++u) {
-      if (t0 + u >= count) continue;
-      const V *src = reinterpret_cast<const V *>(packet + (t0 + u) * kb);
+      if (tok(u) >= count) continue;
+      const V *src = reinterpret_cast<const V *>(packet + tok(u) * kb);
 #pragma unroll
       for (int k = 0; k < kKeyVecs; ++k)
         if (gl + k * kC8Group < nv) x[u][k] = src[gl + k * kC8Group];
@@ -116,7 +126,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   int64_t phys[kC8Unroll];
 #pragma unroll
   for (int u = 0; u < kC8Unroll; ++u) {
-    const int64_t t = t0 + u;
+    const int64_t t = tok(u);
     phys[u] = -1;
     if (t >= count) continue;
     const int64_t slot = c8_index(job.slots, job.slot_i32, start + t);
@@ -142,7 +152,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
 #pragma unroll
     for (int u = 0; u < kC8Unroll; ++u) {
       if (phys[u] < 0) continue;
-      V *dst = reinterpret_cast<V *>(job.from_npu ? packet + (t0 + u) * kb : L.keys + phys[u] * kb);
+      V *dst = reinterpret_cast<V *>(job.from_npu ? packet + tok(u) * kb : L.keys + phys[u] * kb);
 #pragma unroll
       for (int k = 0; k < kKeyVecs; ++k)
         if (gl + k * kC8Group < nv) dst[gl + k * kC8Group] = x[u][k];
@@ -151,7 +161,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
 #pragma unroll
     for (int u = 0; u < kC8Unroll; ++u) {
       if (phys[u] < 0) continue;
-      uint8_t *pk = reinterpret_cast<uint8_t *>(packet) + (t0 + u) * kb;
+      uint8_t *pk = reinterpret_cast<uint8_t *>(packet) + tok(u) * kb;
       uint8_t *ck = reinterpret_cast<uint8_t *>(L.keys) + phys[u] * kb;
       uint8_t *dst = job.from_npu ? pk : ck;
       const uint8_t *src = job.from_npu ? ck : pk;
@@ -166,7 +176,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
     for (int u = 0; u < kC8Unroll; ++u)
       if (gl == u) ph = phys[u];
     if (ph >= 0) {
-      const int64_t t = t0 + gl;
+      const int64_t t = tok(gl);
       uint8_t *ps = reinterpret_cast<uint8_t *>(packet) + count * kb + t * 2;
       uint8_t *cs = reinterpret_cast<uint8_t *>(L.scales) + ph * 2;
       uint8_t *d = job.from_npu ? ps : cs;
