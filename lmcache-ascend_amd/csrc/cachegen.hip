@@ -29,6 +29,7 @@
 // decode table) live in LDS as [symbol][lane] so every lane works in its own
 // column without bank conflicts or barriers.
 #include "common.h"
+#include "cachegen_decode.h"
 
 namespace lmc {
 
@@ -591,15 +592,20 @@ __global__ void __launch_bounds__(kEncTileThreads)
 // loads, so the per-symbol loop touches no global memory except for
 // streams that do not fit the window.
 //
-// Symbol lookup (rule L6) is table driven.  Bases are multiples of 16, so
-// the top 12 bits of the 16-bit window decide the symbol.  L1 has one
-// entry per 7-bit prefix: symbol | length << 8 when one symbol owns the
-// prefix's whole range; 0x8000 | k << 8 | s_first when symbol boundaries
-// fall inside it, k naming one of the stream's kSubTables L2 tables whose
-// 32 one-byte entries (next 5 bits) hold (s - s_first) << 4 | length; and
-// kOverflow when the stream ran out of L2 tables (or a prefix spans more
-// than 16 symbols), which falls back to a binary search over the bases.
-constexpr int kDecLanes = 64;
+// Symbol lookup (rule L6) is table driven, with per-stream tables built in
+// LDS from the staged rows.  n_bins <= 32 takes cgdec::ByteTables: one byte
+// per 8-bit window prefix, so every code of at most 8 bits (all of them for
+// chunks of up to 256 tokens) is one LDS read, and the table is built
+// without data-dependent loops.  Larger n_bins take DecTables below.  Bases
+// are multiples of 16, so the top 12 bits of the 16-bit window decide the
+// symbol.  DecTables' L1 has one entry per 7-bit prefix: symbol | length <<
+// 8 when one symbol owns the prefix's whole range; 0x8000 | k << 8 |
+// s_first when symbol boundaries fall inside it, k naming one of the
+// stream's kSubTables L2 tables whose 32 one-byte entries (next 5 bits)
+// hold (s - s_first) << 4 | length; and kOverflow when the stream ran out
+// of L2 tables (or a prefix spans more than 16 symbols), which falls back
+// to a binary search over the bases.
+constexpr int kDecLanes = cgdec::kLanes;
 constexpr int kDirectBits = 7;
 constexpr int kSubBits = 5;
 constexpr int kSubTables = 4;
@@ -608,7 +614,6 @@ constexpr int kDecLds = 40 * 1024;
 constexpr int kL1Bytes = (1 << kDirectBits) * kDecLanes * 2;
 constexpr int kL2Bytes = kSubTables * (1 << kSubBits) * kDecLanes;
 constexpr int kObufBytes = 4 * kDecLanes;
-constexpr int kRowsOff = kL1Bytes + kL2Bytes + kObufBytes;
 constexpr int kStageBatch = 8;  // 16-byte loads in flight per lane
 
 // Copies n16 16-byte chunks starting at the 16-byte aligned global address
@@ -643,30 +648,21 @@ __device__ __forceinline__ void stage16(uintptr_t src, int n16, uint8_t *dst) {
   }
 }
 
-// Bases and lengths (rules L1-L3) read straight from a staged raw CDF row.
-// `wrap` is the first symbol whose entry is below its predecessor's (nb if
-// none): it and every later symbol have base 0x10000.
-struct StagedRow {
-  const int16_t *r;
-  int wrap;
-  __device__ __forceinline__ uint32_t base(int s) const {
-    return s >= wrap ? 0x10000u : (static_cast<uint32_t>(static_cast<uint16_t>(r[s])) & 0xFFF0u);
-  }
-  __device__ __forceinline__ int len(int s) const {
-    const int nib = static_cast<uint16_t>(r[s]) & 0xF;
-    if (nib) return nib;
-    const uint32_t w = base(s + 1) - base(s);
-    return w ? kPrec - (31 - __builtin_clz(w)) : 0;
-  }
-};
+using cgdec::StagedRow;
 
 // Per-lane decode tables: L1 and L2 columns of stride kDecLanes.
 struct DecTables {
+  static constexpr int kBytes = kL1Bytes + kL2Bytes;
   uint16_t *l1;
   uint8_t *l2;
   StagedRow row;
   int nb;
   int top;  // largest power of two below nb (1 if nb <= 2)
+
+  __device__ __forceinline__ void bind(uint8_t *lds, int lane) {
+    l1 = reinterpret_cast<uint16_t *>(lds) + lane;
+    l2 = lds + kL1Bytes + lane;
+  }
 
   // Builds L1/L2 from the staged row in one pass over the symbols (a loop
   // every lane runs in step).  Symbol s owns the windows [lo, hi): lo is
@@ -799,7 +795,8 @@ __device__ __forceinline__ uint32_t clip_word(uint32_t w, uint32_t q, uint32_t h
 // symbol reads the window dword at q (the next one to append) alongside its
 // L1 read, and the following symbol appends it when 32 bits or fewer are
 // left, so no LDS latency beyond the table lookup sits on the chain.
-__device__ __forceinline__ void decode_block_fast(const DecTables &tb, int T, int C,
+template <class Tab>
+__device__ __forceinline__ void decode_block_fast(const Tab &tb, int T, int C,
                                                   const uint32_t *win, uint32_t win_last,
                                                   uint32_t lo, uint32_t hi, uint8_t *obuf,
                                                   uint8_t *__restrict__ out_blk) {
@@ -848,8 +845,8 @@ __device__ __forceinline__ void decode_block_fast(const DecTables &tb, int T, in
 // from a_lo to a_hi, read with the index clamped into the window.
 // Otherwise dwords come from global memory, and only those holding a byte
 // of [lo, hi) are read.
-template <bool kWin>
-__device__ __forceinline__ void decode_stream(const DecTables &tb, int T, int C,
+template <bool kWin, class Tab>
+__device__ __forceinline__ void decode_stream(const Tab &tb, int T, int C,
                                               const uint8_t *__restrict__ bytes, const uint32_t *win,
                                               uintptr_t a_lo, uintptr_t a_hi, uintptr_t lo,
                                               uintptr_t hi, uint8_t *__restrict__ o) {
@@ -882,14 +879,16 @@ __device__ __forceinline__ void decode_stream(const DecTables &tb, int T, int C,
   }
 }
 
+template <class Tab>
 __global__ void __launch_bounds__(kDecLanes)
     decode_kernel(const int16_t *__restrict__ cdf,
                   const uint8_t *__restrict__ bytes, int64_t nbytes,
                   const int32_t *__restrict__ prefix, int T, int C, int nb,
                   uint8_t *__restrict__ out, int tiles) {
-  // [L1 u16][L2 u8][obuf: 4 tokens x 64 lanes][staged rows][byte window]
+  // [tables][obuf: 4 tokens x 64 lanes][staged rows][byte window]
   extern __shared__ uint32_t lds_words[];
   uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
+  constexpr int kRowsOff = Tab::kBytes + kObufBytes;
   const int rows_cap = ((nb + 1) * kDecLanes * 2 + 32 + 15) & ~15;
   const int win_off = kRowsOff + rows_cap;
   const int win_cap = (kDecLds - win_off) & ~15;
@@ -930,9 +929,8 @@ __global__ void __launch_bounds__(kDecLanes)
   const bool fast = cnt == kDecLanes && (reinterpret_cast<uintptr_t>(out) & 3) == 0 && (C & 3) == 0 &&
                     __all(in_win);
   if (!live) return;
-  DecTables tb;
-  tb.l1 = reinterpret_cast<uint16_t *>(lds) + threadIdx.x;
-  tb.l2 = lds + kL1Bytes + threadIdx.x;
+  Tab tb;
+  tb.bind(lds, static_cast<int>(threadIdx.x));
   tb.row.r = reinterpret_cast<const int16_t *>(lds + kRowsOff + (R0 - r_lo)) + threadIdx.x * (nb + 1);
   tb.nb = nb;
   tb.build();
@@ -941,7 +939,7 @@ __global__ void __launch_bounds__(kDecLanes)
   if (fast) {
     decode_block_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
                       static_cast<uint32_t>(lo - a_lo), static_cast<uint32_t>(hi - a_lo),
-                      lds + kL1Bytes + kL2Bytes, out_blk);
+                      lds + Tab::kBytes, out_blk);
   } else if (in_win) {
     decode_stream<true>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + threadIdx.x);
   } else {
@@ -1128,7 +1126,9 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf_t,
     DeviceGuard guard(bs.device);
     const int tiles = static_cast<int>((C + kDecLanes - 1) / kDecLanes);
     const size_t lds = kDecLds;
-    hipLaunchKernelGGL(decode_kernel, dim3(L * tiles), dim3(kDecLanes), lds,
+    auto kernel = nb <= cgdec::ByteTables::kMaxBins ? decode_kernel<cgdec::ByteTables>
+                                                    : decode_kernel<DecTables>;
+    hipLaunchKernelGGL(kernel, dim3(L * tiles), dim3(kDecLanes), lds,
                        static_cast<hipStream_t>(stream),
                        static_cast<const int16_t *>(cdf.data),
                        static_cast<const uint8_t *>(bs.data), numel(bs),

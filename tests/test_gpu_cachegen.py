@@ -219,15 +219,16 @@ def test_decode_limits(ops):
         ops.decode_fast_new(None, None, None, None)
 
 
-def _arbitrary_cdf_rows(rng, L, C, nb):
+def _arbitrary_cdf_rows(rng, L, C, nb, step=16):
     """CDF rows a caller may build by hand: non-decreasing 16-bit bases in
-    steps of 16 with gaps and repeats anywhere, a first base above zero in
-    some rows, length nibbles 0 (derived from the width) to 15, and in some
-    rows a decreasing entry after which every base reads as 0x10000."""
+    multiples of `step` with gaps and repeats anywhere, a first base above
+    zero in some rows, length nibbles 0 (derived from the width) to 15, and
+    in some rows a decreasing entry after which every base reads as
+    0x10000."""
     rows = np.zeros((L, C, nb + 1), np.uint16)
     for l in range(L):
         for c in range(C):
-            bases = np.sort(rng.integers(0, 0x1000, size=nb)) * 16
+            bases = np.sort(rng.integers(0, 0x10000 // step, size=nb)) * step
             if c % 3 == 0:
                 bases[0] = 0
             nib = rng.integers(0, 16, size=nb)
@@ -240,13 +241,16 @@ def _arbitrary_cdf_rows(rng, L, C, nb):
     return rows.view(np.int16)
 
 
-@pytest.mark.parametrize("nb", [2, 3, 17, 40, 63])
-def test_decode_arbitrary_cdf_rows_vs_oracle(ops, nb):
+@pytest.mark.parametrize("step", [16, 256])
+@pytest.mark.parametrize("nb", [2, 3, 17, 31, 32, 33, 40, 63])
+def test_decode_arbitrary_cdf_rows_vs_oracle(ops, nb, step):
     """Random byte streams of random lengths (zero included) decoded under
-    hand-built CDF rows, bit-exact against the oracle."""
-    rng = np.random.default_rng(100 + nb)
+    hand-built CDF rows, bit-exact against the oracle.  Bases in steps of
+    16 put symbol boundaries inside most 8-bit window prefixes; steps of 256
+    keep them on prefix boundaries, so short codes resolve in one lookup."""
+    rng = np.random.default_rng(100 + nb + step)
     L, C, T = 2, 64, 96
-    cdf = _arbitrary_cdf_rows(rng, L, C, nb)
+    cdf = _arbitrary_cdf_rows(rng, L, C, nb, step)
     lengths = rng.integers(0, 60, size=L * C)
     lengths[::7] = 0
     prefix = np.cumsum(lengths).astype(np.int32).reshape(L, C)
