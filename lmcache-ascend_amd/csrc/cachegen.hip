@@ -840,6 +840,56 @@ __device__ __forceinline__ void decode_block_fast(const Tab &tb, int T, int C,
   }
 }
 
+
+// Fast path of the byte tables: every stream of the block lies in the window
+// and no table entry is an escape, so each symbol is one LDS read and the
+// loop has no branches (cgdec::BitCursor, cgdec::ByteTables::step).
+// Symbols go through the 4-token LDS transpose as in decode_block_fast.
+__device__ __forceinline__ void decode_block_bytes(const cgdec::ByteTables &tb, int T, int C,
+                                                   const uint32_t *win, uint32_t win_last,
+                                                   uint32_t lo, uint32_t hi, uint8_t *obuf,
+                                                   uint8_t *__restrict__ out_blk) {
+  const int lane = static_cast<int>(threadIdx.x);
+  cgdec::BitCursor cur;
+  cur.start(win, win_last, lo, hi);
+  auto step = [&]() -> uint32_t { return tb.step(cur); };
+  // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
+  uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
+  const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
+  int t = 0;
+  for (; t + 4 <= T; t += 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
+    __syncthreads();
+    *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    odst += step4;
+    __syncthreads();
+  }
+  if (t < T) {
+    for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
+    __syncthreads();
+    if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+  }
+}
+
+// Blocks whose streams all fit the window: byte tables without an escape
+// entry in any lane take the branch-free loop, every other block the loop
+// with the escape branch.
+__device__ __forceinline__ void decode_fast(const cgdec::ByteTables &tb, int T, int C,
+                                            const uint32_t *win, uint32_t win_last, uint32_t lo,
+                                            uint32_t hi, uint8_t *obuf, uint8_t *__restrict__ out_blk) {
+  if (__any(tb.escapes))
+    decode_block_fast(tb, T, C, win, win_last, lo, hi, obuf, out_blk);
+  else
+    decode_block_bytes(tb, T, C, win, win_last, lo, hi, obuf, out_blk);
+}
+
+__device__ __forceinline__ void decode_fast(const DecTables &tb, int T, int C, const uint32_t *win,
+                                            uint32_t win_last, uint32_t lo, uint32_t hi, uint8_t *obuf,
+                                            uint8_t *__restrict__ out_blk) {
+  decode_block_fast(tb, T, C, win, win_last, lo, hi, obuf, out_blk);
+}
+
 // One stream occupying [lo, hi) (addresses), symbols to o[0], o[C], ...
 // kWin: every dword the stream needs is in the LDS window holding the bytes
 // from a_lo to a_hi, read with the index clamped into the window.
@@ -937,7 +987,7 @@ __global__ void __launch_bounds__(kDecLanes)
   const uint32_t *win = reinterpret_cast<const uint32_t *>(lds + win_off);
   uint8_t *out_blk = out + static_cast<int64_t>(l) * T * C + c0;
   if (fast) {
-    decode_block_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
+    decode_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
                       static_cast<uint32_t>(lo - a_lo), static_cast<uint32_t>(hi - a_lo),
                       lds + Tab::kBytes, out_blk);
   } else if (in_win) {

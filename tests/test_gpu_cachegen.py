@@ -261,3 +261,26 @@ def test_decode_arbitrary_cdf_rows_vs_oracle(ops, nb, step):
                             torch.from_numpy(prefix).to(DEV), out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("T", [5, 256])
+def test_decode_random_streams_under_calculated_cdfs(ops, T):
+    """Tables from calculate_cdf on 256-token chunks hold no escape entry,
+    so whole blocks take the branch-free decode loop; random byte streams of
+    random lengths (zero, shorter than the symbols need, longer) check its
+    reads at and past each stream's end against the oracle."""
+    rng = np.random.default_rng(7 + T)
+    L, C, nb = 2, 128, 32
+    syms = np.minimum(np.abs(rng.normal(0, 4, size=(L, 256, C))), nb - 2).astype(np.uint8)
+    cdf = oc.calculate_cdf(syms, nb)
+    lengths = rng.integers(0, 200, size=L * C)
+    lengths[::9] = 0
+    lengths[1::9] = 1
+    prefix = np.cumsum(lengths).astype(np.int32).reshape(L, C)
+    stream = rng.integers(0, 256, size=int(lengths.sum()), dtype=np.uint8)
+    want = oc.decode(cdf, stream, prefix, T)
+    out = torch.full((L, T, C), 0xEE, dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(torch.from_numpy(cdf).to(DEV), torch.from_numpy(stream).to(DEV),
+                            torch.from_numpy(prefix).to(DEV), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
