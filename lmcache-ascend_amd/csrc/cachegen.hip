@@ -614,37 +614,43 @@ constexpr int kDecLds = 40 * 1024;
 constexpr int kL1Bytes = (1 << kDirectBits) * kDecLanes * 2;
 constexpr int kL2Bytes = kSubTables * (1 << kSubBits) * kDecLanes;
 constexpr int kObufBytes = 4 * kDecLanes;
-constexpr int kStageBatch = 8;  // 16-byte loads in flight per lane
+constexpr int kRowChunks = 5;   // 16-byte row chunks per lane and load batch (33 x 64 x 2 B)
+constexpr int kWinChunks = 12;  // 16-byte window chunks per lane and load batch (12 KiB)
 
-// Copies n16 16-byte chunks starting at the 16-byte aligned global address
-// `src` into LDS with every lane of the block, kStageBatch loads per lane
-// in flight.  Indexes past the end are clamped to the last chunk, whose
-// slot then receives the same bytes from several lanes.  kSwap stores each
-// dword byte-reversed (big-endian order of the stream bits).
-template <bool kSwap>
-__device__ __forceinline__ void stage16(uintptr_t src, int n16, uint8_t *dst) {
-  const uint4 *s = reinterpret_cast<const uint4 *>(src);
-  uint4 *d = reinterpret_cast<uint4 *>(dst);
-  for (int j0 = 0; j0 < n16; j0 += kDecLanes * kStageBatch) {
-    int idx[kStageBatch];
-    uint4 v[kStageBatch];
+// Loads up to kDecLanes * N 16-byte chunks [j0, j0 + 64 N) of a run of n
+// chunks at the 16-byte aligned global address src into registers, one
+// chunk per lane and slot; indexes past the run are clamped to its last
+// chunk (n >= 1).
+// Global (not flat) loads: they are counted by vmcnt alone and return in
+// order, so a store of an early chunk waits only for the loads before it.
+typedef uint32_t chunk16 __attribute__((ext_vector_type(4)));
+using global_chunk16 = const __attribute__((address_space(1))) chunk16;
+
+template <int N>
+__device__ __forceinline__ void load_chunks(uintptr_t src, int n, int j0, int lane, chunk16 (&v)[N]) {
 #pragma unroll
-    for (int k = 0; k < kStageBatch; ++k) {
-      const int j = j0 + k * kDecLanes + static_cast<int>(threadIdx.x);
-      idx[k] = j < n16 ? j : n16 - 1;
-      v[k] = s[idx[k]];
-    }
+  for (int k = 0; k < N; ++k) {
+    const int j = j0 + k * kDecLanes + lane;
+    v[k] = reinterpret_cast<global_chunk16 *>(src)[j < n ? j : n - 1];
+  }
+}
+
+// Stores the chunks of load_chunks to LDS at dst (several lanes may store
+// the same clamped last chunk, with the same bytes); kSwap byte-reverses
+// each dword (the big-endian order of the stream bits).
+template <bool kSwap, int N>
+__device__ __forceinline__ void store_chunks(uint8_t *dst, int n, int j0, int lane, const chunk16 (&v)[N]) {
 #pragma unroll
-    for (int k = 0; k < kStageBatch; ++k) {
-      uint4 w = v[k];
-      if (kSwap) {
-        w.x = __builtin_bswap32(w.x);
-        w.y = __builtin_bswap32(w.y);
-        w.z = __builtin_bswap32(w.z);
-        w.w = __builtin_bswap32(w.w);
-      }
-      d[idx[k]] = w;
+  for (int k = 0; k < N; ++k) {
+    const int j = j0 + k * kDecLanes + lane;
+    chunk16 w = v[k];
+    if (kSwap) {
+      w.x = __builtin_bswap32(w.x);
+      w.y = __builtin_bswap32(w.y);
+      w.z = __builtin_bswap32(w.z);
+      w.w = __builtin_bswap32(w.w);
     }
+    reinterpret_cast<chunk16 *>(dst)[j < n ? j : n - 1] = w;
   }
 }
 
@@ -671,7 +677,10 @@ struct DecTables {
   // entry; a prefix holding a boundary is opened by the symbol covering its
   // start and filled by that symbol and the following ones.  Also finds
   // row.wrap.
-  __device__ __forceinline__ void build() {
+  __device__ __forceinline__ void clear() {}   // build() writes every entry
+  __device__ __forceinline__ void finish() {}  // build() sets row.wrap and top
+
+  __device__ __forceinline__ void build(uint8_t *) {
     constexpr uint32_t span = 1u << (kPrec - kDirectBits);
     constexpr uint32_t sub = 1u << (kPrec - kDirectBits - kSubBits);
     row.wrap = nb;
@@ -789,6 +798,15 @@ __device__ __forceinline__ uint32_t clip_word(uint32_t w, uint32_t q, uint32_t h
   return k >= 4 ? w : (w & ~(~0u >> (8 * k)));
 }
 
+// Orders a wave's LDS writes before its later reads of other lanes' words.
+// Decode blocks are one wave, and a wave's LDS accesses are performed in
+// order, so no block barrier is needed.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // All 64 streams of the block lie in the window: L1/L2 lookups and symbols
 // transposed through LDS so each lane stores one dword (4 channels of one
 // token) per 4 tokens.  The bit window is refilled without branches: every
@@ -828,14 +846,14 @@ __device__ __forceinline__ void decode_block_fast(const Tab &tb, int T, int C,
   for (; t + 4 <= T; t += 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
-    __syncthreads();
+    wave_sync();
     *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
     odst += step4;
-    __syncthreads();
+    wave_sync();
   }
   if (t < T) {
     for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
-    __syncthreads();
+    wave_sync();
     if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
   }
 }
@@ -851,8 +869,8 @@ __device__ __forceinline__ void decode_block_bytes(const cgdec::ByteTables &tb, 
                                                    uint8_t *__restrict__ out_blk) {
   const int lane = static_cast<int>(threadIdx.x);
   cgdec::BitCursor cur;
-  cur.start(win, win_last, lo, hi);
-  auto step = [&]() -> uint32_t { return tb.step(cur); };
+  cur.start(win, win_last, 8 * lo, hi);
+  auto step = [&]() -> uint32_t { return tb.step(cur) >> 3; };
   // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
   uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
   const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
@@ -860,14 +878,14 @@ __device__ __forceinline__ void decode_block_bytes(const cgdec::ByteTables &tb, 
   for (; t + 4 <= T; t += 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
-    __syncthreads();
+    wave_sync();
     *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
     odst += step4;
-    __syncthreads();
+    wave_sync();
   }
   if (t < T) {
     for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
-    __syncthreads();
+    wave_sync();
     if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
   }
 }
@@ -878,10 +896,13 @@ __device__ __forceinline__ void decode_block_bytes(const cgdec::ByteTables &tb, 
 __device__ __forceinline__ void decode_fast(const cgdec::ByteTables &tb, int T, int C,
                                             const uint32_t *win, uint32_t win_last, uint32_t lo,
                                             uint32_t hi, uint8_t *obuf, uint8_t *__restrict__ out_blk) {
-  if (__any(tb.escapes))
-    decode_block_fast(tb, T, C, win, win_last, lo, hi, obuf, out_blk);
-  else
+  if (__any(tb.escapes)) {
+    cgdec::ByteTables t = tb;
+    t.finish();
+    decode_block_fast(t, T, C, win, win_last, lo, hi, obuf, out_blk);
+  } else {
     decode_block_bytes(tb, T, C, win, win_last, lo, hi, obuf, out_blk);
+  }
 }
 
 __device__ __forceinline__ void decode_fast(const DecTables &tb, int T, int C, const uint32_t *win,
@@ -929,72 +950,121 @@ __device__ __forceinline__ void decode_stream(const Tab &tb, int T, int C,
   }
 }
 
+// Stream geometry of one decode block: lane i of a wave owns stream
+// s0 + i; bytes of the block's streams are [B0, B1) of the byte buffer.
+struct DecBlock {
+  int l, c0, cnt;
+  int64_t s0, start, end, B0, B1;
+  uintptr_t R0, R1, r_lo;
+
+  __device__ __forceinline__ void init(const int16_t *cdf, int64_t nbytes, const int32_t *prefix,
+                                       int C, int nb, int tiles, int lane) {
+    l = blockIdx.x / tiles;
+    c0 = (blockIdx.x % tiles) * kDecLanes;
+    cnt = C - c0 < kDecLanes ? C - c0 : kDecLanes;
+    s0 = static_cast<int64_t>(l) * C + c0;
+    const int64_t stream = s0 + (lane < cnt ? lane : 0);
+    auto clampb = [&](int64_t x) { return x < 0 ? 0 : (x > nbytes ? nbytes : x); };
+    start = clampb(stream == 0 ? 0 : prefix[stream - 1]);
+    end = clampb(prefix[stream]);
+    end = end < start ? start : end;
+    B0 = clampb(s0 == 0 ? 0 : prefix[s0 - 1]);
+    B1 = clampb(prefix[s0 + cnt - 1]);
+    // Rows: bytes [R0, R1) from the 16-byte aligned address at or below R0.
+    R0 = reinterpret_cast<uintptr_t>(cdf + s0 * (nb + 1));
+    R1 = R0 + static_cast<uintptr_t>(cnt) * (nb + 1) * 2;
+    r_lo = R0 & ~uintptr_t(15);
+  }
+
+  // 16-byte chunks of the window staged from a_lo: the block's bytes from
+  // the 16-byte aligned address at or below B0, at most cap bytes.  Every
+  // chunk staged (rows or window) holds a byte of its range, so no load
+  // leaves the buffers' pages.
+  __device__ __forceinline__ int win_chunks(uintptr_t base0, uintptr_t a_lo, int cap) const {
+    if (B1 <= B0) return 0;
+    const uintptr_t want = base0 + B1 - a_lo;
+    const uintptr_t c = static_cast<uintptr_t>(cap);
+    return static_cast<int>(((want < c ? want : c) + 15) >> 4);
+  }
+};
+
+// One wave decodes the block's 64 streams, one lane per stream.
+// LDS: [tables][obuf: 4 tokens x 64 lanes][staged rows][byte window].
+template <class Tab>
+__device__ __forceinline__ void decode_one_wave(uint8_t *lds, const int16_t *__restrict__ cdf,
+                                                const uint8_t *__restrict__ bytes, int64_t nbytes,
+                                                const int32_t *__restrict__ prefix, int T, int C,
+                                                int nb, uint8_t *__restrict__ out, int tiles,
+                                                int lane) {
+  constexpr int kRowsOff = Tab::kBytes + kObufBytes;
+  const int rows_cap = ((nb + 1) * kDecLanes * 2 + 32 + 15) & ~15;
+  const int win_off = kRowsOff + rows_cap;
+  const int win_cap = (kDecLds - win_off) & ~15;
+  DecBlock bk;
+  bk.init(cdf, nbytes, prefix, C, nb, tiles, lane);
+  const int live = lane < bk.cnt;
+  const uintptr_t base0 = reinterpret_cast<uintptr_t>(bytes);
+  const uintptr_t a_lo = (base0 + bk.B0) & ~uintptr_t(15);
+  const int n16 = bk.win_chunks(base0, a_lo, win_cap);
+  const int nrow = static_cast<int>((bk.R1 - bk.r_lo + 15) >> 4);
+  // The rows' loads are issued first and the window's behind them; the
+  // table is built from the stored rows while the window is in flight.
+  chunk16 rv[kRowChunks], wv[kWinChunks];
+  load_chunks(bk.r_lo, nrow, 0, lane, rv);
+  // Without a window the rows' first chunk is loaded and dropped, so no
+  // branch separates these loads from the row stores that wait for rv only.
+  load_chunks(n16 > 0 ? a_lo : bk.r_lo, n16 > 0 ? n16 : 1, 0, lane, wv);
+  Tab tb;
+  tb.bind(lds, lane);
+  tb.clear();
+  store_chunks<false>(lds + kRowsOff, nrow, 0, lane, rv);
+  for (int j0 = kDecLanes * kRowChunks; j0 < nrow; j0 += kDecLanes * kRowChunks) {
+    load_chunks(bk.r_lo, nrow, j0, lane, rv);
+    store_chunks<false>(lds + kRowsOff, nrow, j0, lane, rv);
+  }
+  wave_sync();
+  tb.row.r = reinterpret_cast<const int16_t *>(lds + kRowsOff + (bk.R0 - bk.r_lo)) + lane * (nb + 1);
+  tb.nb = nb;
+  if (live) tb.build(lds + Tab::kBytes + lane);  // obuf byte: scratch for skipped writes
+  if (n16 > 0) {
+    store_chunks<true>(lds + win_off, n16, 0, lane, wv);
+    for (int j0 = kDecLanes * kWinChunks; j0 < n16; j0 += kDecLanes * kWinChunks) {
+      load_chunks(a_lo, n16, j0, lane, wv);
+      store_chunks<true>(lds + win_off, n16, j0, lane, wv);
+    }
+  }
+  wave_sync();
+  const uintptr_t lo = base0 + static_cast<uintptr_t>(bk.start);
+  const uintptr_t hi = base0 + static_cast<uintptr_t>(bk.end);
+  const uintptr_t a_hi = a_lo + 16 * static_cast<uintptr_t>(n16);
+  const bool in_win = hi > lo && (lo & ~uintptr_t(3)) >= a_lo && ((hi + 3) & ~uintptr_t(3)) <= a_hi;
+  const bool fast = bk.cnt == kDecLanes && (reinterpret_cast<uintptr_t>(out) & 3) == 0 && (C & 3) == 0 &&
+                    __all(in_win);
+  if (!live) return;
+  const uint32_t *win = reinterpret_cast<const uint32_t *>(lds + win_off);
+  uint8_t *out_blk = out + static_cast<int64_t>(bk.l) * T * C + bk.c0;
+  if (fast) {
+    decode_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
+                static_cast<uint32_t>(lo - a_lo), static_cast<uint32_t>(hi - a_lo),
+                lds + Tab::kBytes, out_blk);
+  } else {
+    tb.finish();
+    if (in_win)
+      decode_stream<true>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + lane);
+    else
+      decode_stream<false>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + lane);
+  }
+}
+
 template <class Tab>
 __global__ void __launch_bounds__(kDecLanes)
     decode_kernel(const int16_t *__restrict__ cdf,
                   const uint8_t *__restrict__ bytes, int64_t nbytes,
                   const int32_t *__restrict__ prefix, int T, int C, int nb,
                   uint8_t *__restrict__ out, int tiles) {
-  // [tables][obuf: 4 tokens x 64 lanes][staged rows][byte window]
   extern __shared__ uint32_t lds_words[];
-  uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
-  constexpr int kRowsOff = Tab::kBytes + kObufBytes;
-  const int rows_cap = ((nb + 1) * kDecLanes * 2 + 32 + 15) & ~15;
-  const int win_off = kRowsOff + rows_cap;
-  const int win_cap = (kDecLds - win_off) & ~15;
-  const int l = blockIdx.x / tiles;
-  const int c0 = (blockIdx.x % tiles) * kDecLanes;
-  const int cnt = C - c0 < kDecLanes ? C - c0 : kDecLanes;
-  const int64_t s0 = static_cast<int64_t>(l) * C + c0;
-  const int live = static_cast<int>(threadIdx.x) < cnt;
-  const int64_t stream = s0 + (live ? threadIdx.x : 0);
-  auto clampb = [&](int64_t x) { return x < 0 ? 0 : (x > nbytes ? nbytes : x); };
-  int64_t start = clampb(stream == 0 ? 0 : prefix[stream - 1]);
-  int64_t end = clampb(prefix[stream]);
-  end = end < start ? start : end;
-  const int64_t B0 = clampb(s0 == 0 ? 0 : prefix[s0 - 1]);
-  const int64_t B1 = clampb(prefix[s0 + cnt - 1]);
-  // Rows: bytes [R0, R1) from the 16-byte aligned address at or below R0.
-  const uintptr_t R0 = reinterpret_cast<uintptr_t>(cdf + s0 * (nb + 1));
-  const uintptr_t R1 = R0 + static_cast<uintptr_t>(cnt) * (nb + 1) * 2;
-  const uintptr_t r_lo = R0 & ~uintptr_t(15);
-  stage16<false>(r_lo, static_cast<int>((R1 - r_lo + 15) >> 4), lds + kRowsOff);
-  // Window: the block's bytes [B0, B1) from the 16-byte aligned address at
-  // or below B0, at most win_cap bytes.  Every chunk staged (rows or
-  // window) holds a byte of its range, so no load leaves the buffers' pages.
-  const uintptr_t base0 = reinterpret_cast<uintptr_t>(bytes);
-  const uintptr_t a_lo = (base0 + B0) & ~uintptr_t(15);
-  int n16 = 0;
-  if (B1 > B0) {
-    const uintptr_t want = base0 + B1 - a_lo;
-    const uintptr_t cap = static_cast<uintptr_t>(win_cap);
-    n16 = static_cast<int>(((want < cap ? want : cap) + 15) >> 4);
-  }
-  stage16<true>(a_lo, n16, lds + win_off);
-  __syncthreads();
-  const uintptr_t lo = base0 + static_cast<uintptr_t>(start);
-  const uintptr_t hi = base0 + static_cast<uintptr_t>(end);
-  const uintptr_t a_hi = a_lo + 16 * static_cast<uintptr_t>(n16);
-  const bool in_win = hi > lo && (lo & ~uintptr_t(3)) >= a_lo && ((hi + 3) & ~uintptr_t(3)) <= a_hi;
-  const bool fast = cnt == kDecLanes && (reinterpret_cast<uintptr_t>(out) & 3) == 0 && (C & 3) == 0 &&
-                    __all(in_win);
-  if (!live) return;
-  Tab tb;
-  tb.bind(lds, static_cast<int>(threadIdx.x));
-  tb.row.r = reinterpret_cast<const int16_t *>(lds + kRowsOff + (R0 - r_lo)) + threadIdx.x * (nb + 1);
-  tb.nb = nb;
-  tb.build();
-  const uint32_t *win = reinterpret_cast<const uint32_t *>(lds + win_off);
-  uint8_t *out_blk = out + static_cast<int64_t>(l) * T * C + c0;
-  if (fast) {
-    decode_fast(tb, T, C, win, static_cast<uint32_t>(a_hi - a_lo) - 4,
-                      static_cast<uint32_t>(lo - a_lo), static_cast<uint32_t>(hi - a_lo),
-                      lds + Tab::kBytes, out_blk);
-  } else if (in_win) {
-    decode_stream<true>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + threadIdx.x);
-  } else {
-    decode_stream<false>(tb, T, C, bytes, win, a_lo, a_hi, lo, hi, out_blk + threadIdx.x);
-  }
+  decode_one_wave<Tab>(reinterpret_cast<uint8_t *>(lds_words), cdf, bytes, nbytes, prefix, T, C,
+                       nb, out, tiles, static_cast<int>(threadIdx.x));
 }
 
 bool contiguous(const lmc_tensor &t) {
@@ -1176,9 +1246,9 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf_t,
     DeviceGuard guard(bs.device);
     const int tiles = static_cast<int>((C + kDecLanes - 1) / kDecLanes);
     const size_t lds = kDecLds;
-    auto kernel = nb <= cgdec::ByteTables::kMaxBins ? decode_kernel<cgdec::ByteTables>
-                                                    : decode_kernel<DecTables>;
-    hipLaunchKernelGGL(kernel, dim3(L * tiles), dim3(kDecLanes), lds,
+    hipLaunchKernelGGL(nb <= cgdec::ByteTables::kMaxBins ? decode_kernel<cgdec::ByteTables>
+                                                       : decode_kernel<DecTables>,
+                       dim3(L * tiles), dim3(kDecLanes), lds,
                        static_cast<hipStream_t>(stream),
                        static_cast<const int16_t *>(cdf.data),
                        static_cast<const uint8_t *>(bs.data), numel(bs),

@@ -33,25 +33,21 @@ struct StagedRow {
   }
 };
 
-// The 32 bits of {hi, lo} starting s bits below the top of hi, for s in
-// [1, 32] (one v_alignbit_b32).
-__device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t s) {
-  return static_cast<uint32_t>(((static_cast<uint64_t>(hi) << 32) | lo) >> (32 - s));
-}
-
 // Bit cursor over one stream in a window of big-endian dwords (the first
 // stream byte is the top byte of its dword).  The stream occupies window
 // bytes [lo, hi); bytes at or past hi read as zero, and reads past the
 // window's last dword (byte offset `last`) are clamped to it and masked.
-// The next bits sit in three dwords a, b, c with o in [1, 32] bits of a
-// consumed, so the next 32 bits are funnel(a, b, o); q is the window offset
-// of the dword after c, read ahead into `ahead` at every advance so the
-// shift that needs it never waits for it.  An advance of at most 32 bits
-// shifts the dwords at most once.
+// The next bits sit in three dwords a, b, c: the next 32 bits are the 64-bit
+// {a, b} shifted right by sh in [0, 31] (one v_alignbit_b32), so 32 - sh
+// bits of a are consumed.  q is the window offset of the dword after c,
+// read ahead into `ahead` at every advance so the shift that needs it never
+// waits for it.  An advance of at most 32 bits shifts the dwords at most
+// once.
 struct BitCursor {
   const uint32_t *win;
   uint32_t last, hi;
-  uint32_t a, b, c, ahead, o, q;
+  uint32_t a, b, c, ahead, q;
+  int sh;
 
   __device__ __forceinline__ uint32_t word(uint32_t at) const {
     const int d = static_cast<int>(hi) - static_cast<int>(at);
@@ -60,20 +56,22 @@ struct BitCursor {
     return win[(at < last ? at : last) >> 2] & live;
   }
 
-  __device__ __forceinline__ void start(const uint32_t *w, uint32_t w_last, uint32_t lo,
+  // Starts at window bit `bit` (bit 0 is the top bit of the first byte).
+  __device__ __forceinline__ void start(const uint32_t *w, uint32_t w_last, uint32_t bit,
                                         uint32_t end) {
     win = w;
     last = w_last;
     hi = end;
-    q = lo & ~3u;
-    o = 8 * (lo & 3u);
+    q = (bit >> 5) << 2;
+    const uint32_t o = bit & 31u;
     a = 0;
-    if (o == 0) {  // start at the top of b: o = 32 of a dword a that is never read
-      o = 32;
+    if (o == 0) {  // the top of b is next: a (never read) fully consumed
+      sh = 0;
       b = word(q);
       c = word(q + 4);
       q += 8;
     } else {
+      sh = static_cast<int>(32 - o);
       a = word(q);
       b = word(q + 4);
       c = word(q + 8);
@@ -82,16 +80,22 @@ struct BitCursor {
     ahead = word(q);
   }
 
-  __device__ __forceinline__ uint32_t peek32() const { return funnel(a, b, o); }
+  __device__ __forceinline__ uint32_t peek32() const {
+    return static_cast<uint32_t>(((static_cast<uint64_t>(a) << 32) | b) >> sh);
+  }
 
-  __device__ __forceinline__ void advance(uint32_t n) {
-    o += n;
-    const bool sh = o > 32;
-    a = sh ? b : a;
-    b = sh ? c : b;
-    c = sh ? ahead : c;
-    o -= sh ? 32u : 0u;
-    q += sh ? 4u : 0u;
+  // Window bit of the next symbol (a holds the dword at byte q - 12).
+  __device__ __forceinline__ uint32_t bitpos() const { return 8 * (q - 12) + 32 - sh; }
+
+  // Consumes n (<= 32) bits.
+  __device__ __forceinline__ void advance(int n) {
+    sh -= n;
+    const bool s = sh < 0;
+    a = s ? b : a;
+    b = s ? c : b;
+    c = s ? ahead : c;
+    sh &= 31;
+    q += s ? 4u : 0u;
     ahead = word(q);
   }
 };
@@ -100,26 +104,29 @@ struct BitCursor {
 // window (256 per stream).  An entry is (s << 3) | (len - 1) when every
 // window with that prefix decodes to symbol s of length 1..8, and kEscape
 // (0xFF) otherwise: a symbol base strictly inside the prefix's range, a
-// code longer than 8 bits or of length 0, or symbol 31 of length 8, the
-// one code that would read as kEscape.  Escaped windows take a binary
-// search over the bases.  Codes of calculate_cdf's rule on chunks of up to
-// 256 tokens are at most 8 bits long and their bases are multiples of 256,
-// so their tables hold no escapes.
+// code longer than 8 bits or of length 0, or symbol 31 of length 8, the one
+// code that would read as kEscape.  Escaped windows take a binary search
+// over the bases.  Codes of calculate_cdf's rule on chunks of up to 256
+// tokens are at most 8 bits long and their bases are multiples of 256, so
+// their tables hold no escapes.
 //
 // Layout: entry e of the lane's stream is byte (e / 4) * 256 + lane * 4 +
 // e % 4 of the block's 16 KiB table, so a lane's four consecutive entries are
-// one dword and the 64 lanes' lookups hit 64 distinct dwords.
+// one dword (the build scans dwords) and the 64 lanes' lookups hit 64
+// distinct dwords; the byte offset is ((e << 6) | e) & 0x3F03 plus lane * 4.
 //
-// Build (no data-dependent loops): every symbol s >= 1 with a base b below
-// 0x10000 writes its entry at prefix ceil(b / 256), where it becomes the
-// decoded symbol, and kEscape at prefix floor(b / 256) when b is not a
-// multiple of 256; symbols are taken in increasing order, so a later write
-// at the same prefix wins, which is the larger symbol, as rule L6 wants.
-// A scan then carries each written entry forward over the unwritten (zero)
-// prefixes after it, starting from symbol 0's entry.  An escape written for
-// a boundary is always followed by a written entry (the same symbol's, at
-// the next prefix), so it never spreads; an escape written as a symbol's
-// entry spreads exactly over that symbol's prefixes.
+// Build (no data-dependent loops): clear() zeroes the table; mark(), for
+// every symbol s >= 1 with a base b below 0x10000, writes its entry at prefix
+// ceil(b / 256), where it becomes the decoded symbol, and kEscape at prefix
+// floor(b / 256) when b is not a multiple of 256; symbols are taken in
+// increasing order, so a later write at the same prefix wins, which is the
+// larger symbol, as rule L6 wants; symbol 0, which also owns the windows
+// below the first base, is written at prefix 0.  scan() then carries each
+// written entry forward over the unwritten (zero) prefixes after it.
+// Entries grow with s, and s grows with the prefix, so that is a running
+// maximum.  Once an escape has been written, the running maximum turns every
+// later entry into an escape as well; those take the binary search, so each
+// entry is either exact or an escape.
 struct ByteTables {
   static constexpr int kBytes = 256 * kLanes;
   static constexpr uint32_t kEscape = 0xFFu;
@@ -128,8 +135,8 @@ struct ByteTables {
   uint8_t *tab;  // block table + lane * 4
   StagedRow row;
   int nb;
-  int top;      // largest power of two below nb (1 if nb <= 2)
-  bool escapes;  // some entry is kEscape (set by build)
+  int top;       // largest power of two below nb (1 if nb <= 2)
+  bool escapes;  // some scanned entry is kEscape
 
   __device__ __forceinline__ void bind(uint8_t *lds, int lane) { tab = lds + lane * 4; }
 
@@ -137,69 +144,95 @@ struct ByteTables {
     return tab + (e >> 2) * (kLanes * 4) + (e & 3u);
   }
 
-  __device__ __forceinline__ void build() {
+  __device__ __forceinline__ void clear() {
     uint32_t *t32 = reinterpret_cast<uint32_t *>(tab);
     for (int d = 0; d < 64; ++d) t32[d * kLanes] = 0;
-    row.wrap = nb;
-    uint32_t raw = static_cast<uint16_t>(row.r[0]);
-    uint32_t base = raw & 0xFFF0u;
-    uint32_t last = base;  // last base before any wrap
-    uint32_t code0 = kEscape;
-    for (int s = 0; s < nb; ++s) {
-      uint32_t next = 0x10000u, next_raw = 0;
-      if (s + 1 < nb) {
-        next_raw = static_cast<uint16_t>(row.r[s + 1]);
-        const uint32_t nbase = next_raw & 0xFFF0u;
-        if (row.wrap == nb && nbase >= last) {
-          next = nbase;
-          last = nbase;
-        } else if (row.wrap == nb) {
-          row.wrap = s + 1;
-        }
+  }
+
+  // Writes the entries of the cleared table and sets row.wrap.  The row is
+  // read into registers (kMaxBins entries whatever nb is: entries past the
+  // row are garbage and lie past the wrap); a first pass finds the wrap,
+  // the first symbol whose base is below an earlier one, or nb; every
+  // symbol from the wrap on has base 0x10000 and writes nothing.  Writes
+  // that fall outside the table go to `dummy`, a byte of the caller's, so
+  // the loops have no branches.
+  __device__ __forceinline__ void mark(uint8_t *dummy) {
+    uint32_t rw[kMaxBins];
+#pragma unroll
+    for (int s = 0; s < kMaxBins; ++s) rw[s] = static_cast<uint16_t>(row.r[s]);
+    int wrap = nb;
+    uint32_t top_base = rw[0] & 0xFFF0u;
+#pragma unroll
+    for (int s = 1; s < kMaxBins; ++s) {
+      const uint32_t v = rw[s] & 0xFFF0u;
+      wrap = min(wrap, v < top_base ? s : kMaxBins);
+      top_base = max(top_base, v);
+    }
+    row.wrap = wrap;
+    uint32_t base = rw[0] & 0xFFF0u;
+#pragma unroll
+    for (int s = 0; s < kMaxBins; ++s) {
+      const uint32_t next = s + 1 < wrap ? rw[s + 1 < kMaxBins ? s + 1 : 0] & 0xFFF0u : 0x10000u;
+      const uint32_t nib = rw[s] & 0xFu;
+      const uint32_t w = next - base;
+      // 16 - floor(log2 w); w = 0 gives 17, an escape.
+      const uint32_t wl = static_cast<uint32_t>(w != 0 ? __builtin_clz(w) : 32) - 15u;
+      const uint32_t len = nib != 0 ? nib : wl;
+      const uint32_t code = len - 1u < 8u ? ((static_cast<uint32_t>(s) << 3) | (len - 1u)) : kEscape;
+      if (s == 0) {  // owns the windows below every later base: prefix 0
+        *entry(0) = static_cast<uint8_t>(code);
+      } else {
+        // base is 0x10000 from the wrap on: no escape (its low byte is 0)
+        // and no entry (it is not below 0xFF01).
+        *((base & 0xFFu) ? entry(base >> 8) : dummy) = static_cast<uint8_t>(kEscape);
+        *(base < 0xFF01u ? entry((base + 0xFFu) >> 8) : dummy) = static_cast<uint8_t>(code);
       }
-      int len = static_cast<int>(raw & 0xFu);
-      if (len == 0) {
-        const uint32_t w = next - base;
-        if (w != 0) len = kPrec - (31 - __builtin_clz(w));
-      }
-      const uint32_t code = (len >= 1 && len <= 8)
-                                ? ((static_cast<uint32_t>(s) << 3) | static_cast<uint32_t>(len - 1))
-                                : kEscape;
-      if (s == 0) {
-        code0 = code;
-      } else if (base < 0x10000u) {
-        if (base & 0xFFu) *entry(base >> 8) = static_cast<uint8_t>(kEscape);
-        const uint32_t pos = (base + 0xFFu) >> 8;
-        if (pos < 256u) *entry(pos) = static_cast<uint8_t>(code);
-      }
-      raw = next_raw;
       base = next;
     }
-    uint32_t carry = code0, most = 0;
-    for (int d = 0; d < 64; ++d) {
-      const uint32_t w = t32[d * kLanes];
-      uint32_t o = 0;
+  }
+
+  // Running maximum over dwords [d0, d1) starting from `carry` (the entry
+  // before dword d0, 0 for d0 = 0).
+  __device__ __forceinline__ void scan(int d0, int d1, uint32_t carry) {
+    uint32_t *t32 = reinterpret_cast<uint32_t *>(tab);
+    for (int d = d0; d < d1; d += 8) {
+      uint32_t w[8];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t b = (w >> (8 * k)) & 0xFFu;
-        carry = b ? b : carry;
-        most = most > carry ? most : carry;
-        o |= carry << (8 * k);
+      for (int k = 0; k < 8; ++k) w[k] = t32[(d + k) * kLanes];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        uint32_t o = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t v = (w[k] >> (8 * i)) & 0xFFu;
+          carry = carry > v ? carry : v;
+          o |= carry << (8 * i);
+        }
+        t32[(d + k) * kLanes] = o;
       }
-      t32[d * kLanes] = o;
     }
-    escapes = most == kEscape;
+    escapes = carry == kEscape;
+  }
+
+  // top, which only the binary search reads.
+  __device__ __forceinline__ void finish() {
     top = 1;
     while (top * 2 < nb) top *= 2;
   }
 
+  // Builds the table after clear().
+  __device__ __forceinline__ void build(uint8_t *dummy) {
+    mark(dummy);
+    scan(0, 64, 0);
+  }
+
   // One symbol at the cursor for a table without escapes (one LDS read, no
-  // branches).
+  // branches); returns the entry: symbol e >> 3, length (e & 7) + 1.
   __device__ __forceinline__ uint32_t step(BitCursor &cur) const {
-    const uint32_t w = cur.peek32();
-    const uint32_t e = tab[((w >> 26) << 8) + ((w >> 24) & 3u)];
-    cur.advance((e & 7u) + 1);
-    return e >> 3;
+    const uint32_t e = cur.peek32() >> 24;
+    const uint32_t x = tab[((e << 6) | e) & 0x3F03u];
+    cur.advance(static_cast<int>(x & 7u) + 1);
+    return x;
   }
 
   // Symbol and code length for the 16-bit window v.

@@ -284,3 +284,23 @@ def test_decode_random_streams_under_calculated_cdfs(ops, T):
                             torch.from_numpy(prefix).to(DEV), out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("T", [63, 64, 65, 128, 201, 256])
+@pytest.mark.parametrize("C", [64, 96, 192])
+def test_decode_valid_streams_across_lengths(ops, T, C):
+    """Streams encoded by the oracle from quantised Gaussian symbols, decoded
+    at token counts on both sides of the two-wave decoder's range (64..256)
+    and with a partial last block of channels; bit-exact symbols."""
+    rng = np.random.default_rng(1000 + 7 * T + C)
+    L, nb = 3, 32
+    scale = rng.uniform(0.5, 6.0, size=(1, 1, C))
+    syms = np.clip(np.round(rng.normal(0, 1, size=(L, T, C)) * scale) + 15, 0, 30).astype(np.uint8)
+    cdf = oc.calculate_cdf(syms, nb)
+    enc, lens = oc.encode(cdf, syms, 4 * T)
+    stream, pref = oc.concat_streams(enc, lens)
+    out = torch.full((L, T, C), 0xEE, dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(torch.from_numpy(cdf).to(DEV), torch.from_numpy(stream).to(DEV),
+                            torch.from_numpy(pref).to(DEV), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), syms)
