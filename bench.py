@@ -633,6 +633,23 @@ def main(argv=None):
         extra["d2d_per_chunk_calls_store"] = time_events(torch, stream, store_per_chunk, 10)[0]
         extra["d2d_per_chunk_calls_retrieve"] = time_events(torch, stream, retrieve_per_chunk, 10)[0]
 
+        # The same 16 calls captured once in a HIP graph and replayed: no host
+        # work per call.
+        graphs = {}
+        for name, fn in (("store", store_per_chunk), ("retrieve", retrieve_per_chunk)):
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                fn()
+            stream.wait_stream(side)
+            torch.cuda.synchronize()
+            graphs[name] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[name]):
+                fn()
+            torch.cuda.synchronize()
+        extra["d2d_per_chunk_graph_store"] = time_events(torch, stream, graphs["store"].replay, 10)[0]
+        extra["d2d_per_chunk_graph_retrieve"] = time_events(torch, stream, graphs["retrieve"].replay, 10)[0]
+
     if "call_overhead" in sel:
         # Host time per drop-in call on a 1-token transfer, through the C++
         # binding and through ctypes (wall clock per call, stream not drained).
