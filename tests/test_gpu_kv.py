@@ -626,3 +626,32 @@ def test_binding_and_ctypes_paths_agree(ops):
     _sync()
     assert torch.equal(c.view(torch.int16), d.view(torch.int16))
     assert torch.equal(c.view(torch.int16), a[:, 1].view(torch.int16))
+
+
+def test_zero_token_calls_leave_everything_unchanged(ops):
+    """An empty slot mapping (a chunk with no tokens) is a no-op for every
+    gather/scatter entry point, both directions, and for the K re-rotation:
+    no launch, no error, caches and buffers unchanged."""
+    gen = torch.Generator().manual_seed(21)
+    L, NB, BS, H, D = 2, 8, 16, 2, 128
+    W = H * D
+    pbs = NB * BS
+    layers = _paged(1, L, NB, BS, H, D, gen)
+    ptrs = ptr_table(layers, DEV)
+    before = [x.clone() for x in layers]
+    none = torch.empty(0, dtype=torch.int64, device=DEV)
+    kv = torch.empty((2, L, 0, W), dtype=torch.bfloat16, device=DEV)
+    for direction in (True, False):
+        ops.multi_layer_kv_transfer(kv, ptrs, none, torch.device(DEV), pbs, direction, False, 1, W, W, 0)
+    ops.multi_layer_kv_transfer_batched([kv], ptrs, none, [0], torch.device(DEV), pbs, False, False, 1, W, W, 0)
+    for l in range(L):
+        ops.load_and_reshape_flash(kv, layers[l][0], layers[l][1], none, l)
+        ops.reshape_and_cache_back_flash(kv, layers[l][0], layers[l][1], none, l)
+        ops.single_layer_kv_transfer(torch.empty((2, 0, W), dtype=torch.bfloat16, device=DEV), layers[l],
+                                     none, False, 1, vllm_two_major=True)
+    key = torch.empty((0, W), dtype=torch.bfloat16, device=DEV)
+    cache = torch.zeros((16, D), dtype=torch.bfloat16, device=DEV)
+    ops.rotary_embedding_k_fused(none, none, key, D, cache, True)
+    _sync()
+    for a, b in zip(before, layers):
+        assert torch.equal(a, b)
