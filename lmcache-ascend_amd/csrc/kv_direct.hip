@@ -270,6 +270,105 @@ __global__ void __launch_bounds__(kEntThreads) kv_entry_copy(EntryJob job) {
     copy_entry<VEC, NT>(job, e, gl, G);
 }
 
+// Two entries per group for the flat sparse mode (kSparseFlat, one_pass, no
+// mirror, the flat buffer in device memory).  Every index load of both
+// entries is issued before any is used (indices clamped into their arrays),
+// then both entries' row loads, then the stores: the dependent chain index
+// -> row is paid once for two entries.  The checks are those of resolve()
+// and copy_entry().  Measured on MI355X, 65536 MLA tokens (1024 + 128-byte
+// rows) scattered from a device buffer: 29.6 us against 30.7 us with one
+// entry per group.
+template <int VEC, bool NT>
+__global__ void __launch_bounds__(kEntThreads) kv_entry_pair_copy(EntryJob job) {
+  using V = typename VecOf<VEC>::T;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kEntThreads + threadIdx.x;
+  const int G = 1 << job.group_shift;
+  const int gl = static_cast<int>(gid & (G - 1));
+  const int64_t e0 = (gid >> job.group_shift) * 2;
+  if (e0 >= job.n_entries || (job.counts != nullptr && job.n_rows <= 0)) return;
+  int64_t tok[2], slot[2];
+  bool ok[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int64_t e = e0 + k < job.n_entries ? e0 + k : job.n_entries - 1;
+    tok[k] = load_index(job.tokens, job.tok_i32, e);
+    slot[k] = load_index(job.slots, job.slot_i32, e);
+    ok[k] = e0 + k < job.n_entries;
+    if (job.counts != nullptr) {
+      const int64_t r = e / job.row_width;
+      const int64_t rr = r < job.n_rows ? r : job.n_rows - 1;
+      const int32_t cnt = job.counts[rr * job.count_stride];
+      ok[k] = ok[k] && r < job.n_rows && e - r * job.row_width < cnt;
+    }
+  }
+  int64_t t[2], nc[2];
+  uint64_t lbase[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    ok[k] = ok[k] && slot[k] >= 0 && slot[k] < job.num_slots;
+    ok[k] = ok[k] && tok[k] >= 0 && tok[k] < job.lmc_tokens;
+    t[k] = tok[k];
+    nc[k] = 0;
+    lbase[k] = job.lmc_flat;
+  }
+  uint8_t *src[2][kMaxPlanes], *dst[2][kMaxPlanes];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int p = 0; p < kMaxPlanes; ++p) {
+      src[k][p] = dst[k][p] = nullptr;
+      if (p >= job.n_planes) continue;
+      const PlaneDesc &pd = job.plane[p];
+      uint8_t *lm = reinterpret_cast<uint8_t *>(lbase[k]) + pd.lmc_off_fixed +
+                    pd.lmc_off_per_t * nc[k] + t[k] * pd.lmc_token_stride;
+      int64_t poff = pd.paged_off;
+      if (job.block_size > 0)
+        poff += (slot[k] / job.block_size) * pd.blk_stride + (slot[k] % job.block_size) * pd.row_pitch;
+      else
+        poff += slot[k] * pd.row_pitch;
+      uint8_t *other = reinterpret_cast<uint8_t *>(job.base[p]) + poff;
+      dst[k][p] = job.page2lmc ? lm : other;
+      src[k][p] = job.page2lmc ? other : lm;
+    }
+  // A chunk base that is not VEC-aligned (a device value) moves bytewise.
+  bool vec[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) vec[k] = (lbase[k] & (VEC - 1)) == 0;
+  V x[2][kMaxPlanes][kEntUnroll];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!(ok[k] && vec[k])) continue;
+#pragma unroll
+    for (int p = 0; p < kMaxPlanes; ++p)
+#pragma unroll
+      for (int u = 0; u < kEntUnroll; ++u) {
+        const int v = gl + u * G;
+        if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes)
+          x[k][p][u] = ld<V, NT>(reinterpret_cast<const V *>(src[k][p]) + v);
+      }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!ok[k]) continue;
+    if (vec[k]) {
+#pragma unroll
+      for (int p = 0; p < kMaxPlanes; ++p)
+#pragma unroll
+        for (int u = 0; u < kEntUnroll; ++u) {
+          const int v = gl + u * G;
+          if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes)
+            st<V, NT>(reinterpret_cast<V *>(dst[k][p]) + v, x[k][p][u]);
+        }
+    } else {
+#pragma unroll
+      for (int p = 0; p < kMaxPlanes; ++p) {
+        if (p >= job.n_planes) continue;
+        for (int64_t b = gl; b < job.plane[p].row_bytes; b += G) dst[k][p][b] = src[k][p][b];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -346,14 +445,18 @@ void launch_entries(EntryJob job, bool host_lmc, hipStream_t stream) {
   while ((int64_t(unroll) << shift) < vecs && shift < max_shift) ++shift;
   job.group_shift = shift;
   job.one_pass = vecs <= (int64_t(unroll) << shift);
-  const int64_t threads = job.n_entries << shift;
+  // Flat sparse entries between device buffers go two per group.
+  const bool pair = !host_lmc && job.one_pass && !job.mirror && job.mode == kSparseFlat;
+  const int64_t threads = (pair ? (job.n_entries + 1) / 2 : job.n_entries) << shift;
   int64_t blocks = (threads + kEntThreads - 1) / kEntThreads;
   if (host_read) blocks = std::min<int64_t>(blocks, kEntHostReadBlocks);
   check(blocks < (int64_t(1) << 31), "too many entries in one call");
   const dim3 grid(static_cast<unsigned>(blocks)), block(kEntThreads);
   const bool nt = nontemporal_enabled() && !host_lmc;
 #define LMC_ENTRY_LAUNCH(V)                                                  \
-  if (nt) hipLaunchKernelGGL((kv_entry_copy<V, true>), grid, block, 0, stream, job); \
+  if (pair && nt) hipLaunchKernelGGL((kv_entry_pair_copy<V, true>), grid, block, 0, stream, job); \
+  else if (pair) hipLaunchKernelGGL((kv_entry_pair_copy<V, false>), grid, block, 0, stream, job); \
+  else if (nt) hipLaunchKernelGGL((kv_entry_copy<V, true>), grid, block, 0, stream, job); \
   else hipLaunchKernelGGL((kv_entry_copy<V, false>), grid, block, 0, stream, job);
   switch (vec) {
   case 16: LMC_ENTRY_LAUNCH(16) break;
