@@ -553,7 +553,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct,dma,c8graph",
+    ap.add_argument("--modes", default="d2d,per_chunk,flash,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct,dma,c8graph",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -649,6 +649,26 @@ def main(argv=None):
             torch.cuda.synchronize()
         extra["d2d_per_chunk_graph_store"] = time_events(torch, stream, graphs["store"].replay, 10)[0]
         extra["d2d_per_chunk_graph_retrieve"] = time_events(torch, stream, graphs["retrieve"].replay, 10)[0]
+
+    if "flash" in sel:
+        # load_and_reshape_flash / reshape_and_cache_back_flash: one call per
+        # layer over the 4096 tokens of a [2, L, T, W] buffer, as the
+        # layer-by-layer connector calls them.
+        kvbuf = torch.empty((2, L, n_tok, W), dtype=torch.bfloat16, device=dev)
+
+        def flash_store():
+            for l in range(L):
+                ops.load_and_reshape_flash(kvbuf, flat[2 * l], flat[2 * l + 1], slots, l)
+
+        def flash_retrieve():
+            for l in range(L):
+                ops.reshape_and_cache_back_flash(kvbuf, flat[2 * l], flat[2 * l + 1], slots, l)
+
+        flash_store()
+        flash_retrieve()
+        extra["d2d_flash_per_layer_calls_store"] = time_events(torch, stream, flash_store, 10)[0]
+        extra["d2d_flash_per_layer_calls_retrieve"] = time_events(torch, stream, flash_retrieve, 10)[0]
+        del kvbuf
 
     if "call_overhead" in sel:
         # Host time per drop-in call on a 1-token transfer, through the C++
