@@ -558,7 +558,7 @@ def main(argv=None):
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: this library has no multi-GPU path "
               "(the KV gather/scatter shards per rank with no exchange step).", file=sys.stderr)
         return 2
 

@@ -19,7 +19,7 @@
  *   - decode reads a concatenation of the streams in (layer, channel) order
  *     with inclusive prefix-summed byte lengths (:194-221).
  *
- * Rules this build fixes where the reference leaves them open (the exact
+ * Rules this library fixes where the reference leaves them open (the exact
  * calculate_cdf values are "parity unpinned": only the absent kernel defines
  * them):
  *   L1  low 4 bits of an entry = code length l_s; interval bases are the

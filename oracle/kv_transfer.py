@@ -1,6 +1,6 @@
 """CPU oracle for the paged-KV gather/scatter ops.  TEST INFRASTRUCTURE ONLY.
 
-This module is the checker the tests, `__graft_entry__.smoke()` and the
+This module is the reference the tests, `__graft_entry__.smoke()` and the
 `cpu_baseline` leg of `bench.py` compare the HIP kernels against.  It is
 never on the product path: the `lmcache_amd` package does not import it.
 

@@ -135,7 +135,7 @@ def test_cachegen_kv_chunk_bit_exact(ops):
 @pytest.mark.parametrize("n_layers", [1, 28])
 @pytest.mark.parametrize("num_heads", [1, 8])
 def test_encode_into_decode(ops, n_tokens, n_layers, num_heads):
-    """tests/v1/test_cachegen_kernels.py:242-345 (with this build's quantiser)."""
+    """tests/v1/test_cachegen_kernels.py:242-345 (with this library's quantiser)."""
     C = num_heads * 128
     rng = np.random.default_rng(n_tokens * 31 + n_layers)
     x = rng.normal(0, 2, size=(2 * n_layers, n_tokens, C)).astype(np.float32)

@@ -84,7 +84,7 @@ def test_reference_basic_decode(layers, channels, bits):
 def test_cdf_of_uniform_histogram_is_reference_decode_cdf(bits):
     # 2^n equally frequent symbols: every code is n bits and the CDF is the
     # one test_basic_decode builds (cdf[b] = b * 2^(16-n) | n), except the end
-    # entry, which this build stores as the wrapped 0x10000 = 0.
+    # entry, which this library stores as the wrapped 0x10000 = 0.
     n = 2 ** bits
     syms = np.tile(np.arange(n, dtype=np.uint8), 4).reshape(1, 4 * n, 1)
     cdf = oc.calculate_cdf(syms, n)
