@@ -207,3 +207,57 @@ def test_cachegen_replays_round_trip(ops):
         g_dec.replay()
         torch.cuda.synchronize()
         assert torch.equal(dec, sym), r
+
+
+@pytest.mark.parametrize("host_sources", [False, True])
+def test_sparse_graph_replays_follow_device_counts(ops, host_sources):
+    """sparse_graph_kv_transfer is the reference's graph-replay copy
+    (csrc/graph/sparse_graph_kernel.cpp): captured once, each replay reads
+    the selections, slots, counts and limits the captured tensors hold at
+    that replay.  Every replay writes new values into them and matches the
+    oracle on the same bytes."""
+    import numpy as np
+
+    from kvutil import to_bytes
+    from oracle import kv_transfer as ok
+
+    rng = np.random.default_rng(31 + host_sources)
+    R, W, cs, cpr, KH, PH = 3, 64, 64, 4, 512, 64
+    kb, pb = KH * 2, PH * 2
+    NB, BS = 32, 16
+    k = torch.zeros((NB, BS, 1, KH), dtype=torch.bfloat16, device=DEV)
+    pe = torch.zeros((NB, BS, 1, PH), dtype=torch.bfloat16, device=DEV)
+    srcs_k, srcs_p = [], []
+    for _ in range(R * cpr):
+        a = torch.from_numpy(rng.integers(0, 256, size=cs * kb, dtype=np.uint8))
+        b = torch.from_numpy(rng.integers(0, 256, size=cs * pb, dtype=np.uint8))
+        srcs_k.append(a.pin_memory() if host_sources else a.to(DEV))
+        srcs_p.append(b.pin_memory() if host_sources else b.to(DEV))
+    addr = (lambda t: ops.get_device_ptr(t.data_ptr(), t.numel())) if host_sources else (lambda t: t.data_ptr())
+    ptrs = torch.tensor([[addr(t) for t in srcs_k], [addr(t) for t in srcs_p]], dtype=torch.int64, device=DEV)
+    sel = torch.zeros((R, W), dtype=torch.int32, device=DEV)
+    slots = torch.full((R, W), -1, dtype=torch.int64, device=DEV)
+    counts = torch.zeros((R,), dtype=torch.int32, device=DEV)
+    limits = torch.zeros((R,), dtype=torch.int32, device=DEV)
+    st = ops.prepare_sparse_direct_destination_state((k, pe), torch.zeros(1, device=DEV), 5, 0, 0, 0)
+    g = _capture(lambda: ops.sparse_graph_kv_transfer(st, slots, sel, counts, ptrs, limits, cs))
+    for r in range(REPLAYS):
+        s_np = rng.integers(-2, cs * cpr + 3, size=(R, W)).astype(np.int32)
+        d_np = rng.permutation(NB * BS)[: R * W].reshape(R, W).astype(np.int64)
+        c_np = rng.integers(0, W + 8, size=R).astype(np.int32)
+        l_np = rng.integers(0, cs * cpr + 1, size=R).astype(np.int32)
+        c_np[r % R] = 0
+        sel.copy_(torch.from_numpy(s_np))
+        slots.copy_(torch.from_numpy(d_np))
+        counts.copy_(torch.from_numpy(c_np))
+        limits.copy_(torch.from_numpy(l_np))
+        k.zero_()
+        pe.zero_()
+        want_k, want_p = to_bytes(k), to_bytes(pe)
+        ok.sparse_graph_kv_transfer(want_k, want_p, kb, pb, d_np, s_np, c_np, l_np,
+                                    [to_bytes(t) for t in srcs_k], [to_bytes(t) for t in srcs_p], cs)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_bytes(k), want_k), r
+        assert np.array_equal(to_bytes(pe), want_p), r
+        assert want_k.any(), r
