@@ -261,3 +261,51 @@ def test_sparse_graph_replays_follow_device_counts(ops, host_sources):
         assert np.array_equal(to_bytes(k), want_k), r
         assert np.array_equal(to_bytes(pe), want_p), r
         assert want_k.any(), r
+
+
+@pytest.mark.parametrize("from_npu", [True, False])
+def test_c8_prepared_replays_follow_device_metadata(ops, from_npu):
+    """indexer_c8_transfer_prepared captured once; each replay reads the
+    packet contents, chunk offsets, counts and slots the captured tensors
+    hold at that replay (a zero count and slots outside the cache included)
+    and matches the oracle on the same bytes, in both directions."""
+    import numpy as np
+
+    from kvutil import to_bytes
+    from oracle import kv_transfer as ok
+
+    rng = np.random.default_rng(41 + from_npu)
+    blocks, capacity, chunks = 8, 128, 4
+    keys = torch.zeros((blocks, 128, 1, 128), dtype=torch.int8, device=DEV)
+    scales = torch.zeros((blocks, 128, 1, 1), dtype=torch.float16, device=DEV)
+    packets = [torch.zeros(capacity * 130, dtype=torch.uint8, device=DEV) for _ in range(chunks)]
+    ptrs = torch.tensor([p.data_ptr() for p in packets], dtype=torch.int64, device=DEV)
+    offs = torch.zeros(chunks, dtype=torch.int32, device=DEV)
+    counts = torch.zeros(chunks, dtype=torch.int32, device=DEV)
+    slots = torch.full((chunks * capacity,), -1, dtype=torch.int64, device=DEV)
+    state = ops.IndexerC8State(keys, scales)
+    g = _capture(lambda: ops.indexer_c8_transfer_prepared(state, ptrs, offs, counts, slots, capacity, from_npu))
+    for r in range(REPLAYS):
+        cnt = rng.integers(1, capacity + 1, size=chunks).astype(np.int32)
+        cnt[r % chunks] = 0
+        off = np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(np.int32)
+        n = int(cnt.sum())
+        s_np = np.full(chunks * capacity, -1, np.int64)
+        s_np[:n] = rng.permutation(blocks * 128 + 20)[:n] - 10    # distinct; a few outside the cache
+        keys.copy_(torch.from_numpy(rng.integers(-128, 128, size=tuple(keys.shape), dtype=np.int8)))
+        scales.copy_(torch.from_numpy(rng.integers(0, 65535, size=tuple(scales.shape), dtype=np.uint16)
+                                      .view(np.float16)))
+        for p in packets:
+            p.copy_(torch.from_numpy(rng.integers(0, 256, size=p.numel(), dtype=np.uint8)))
+        offs.copy_(torch.from_numpy(off))
+        counts.copy_(torch.from_numpy(cnt))
+        slots.copy_(torch.from_numpy(s_np))
+        layer = ok.C8Layer(to_bytes(keys), to_bytes(scales), 128, 1, None, blocks * 128)
+        ref_packets = [to_bytes(p) for p in packets]
+        ok.indexer_c8_transfer([layer], [ref_packets], off.tolist(), cnt.tolist(), s_np, capacity, from_npu, False)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_bytes(keys), layer.keys), r
+        assert np.array_equal(to_bytes(scales), layer.scales), r
+        for p, want in zip(packets, ref_packets):
+            assert np.array_equal(to_bytes(p), want), r
