@@ -809,6 +809,9 @@ void single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches, int n,
   job.n_planes = g.n_planes;
   job.block_size = g.block_size;
   job.num_slots = g.num_slots;
+  // The kernels split a block-strided slot into (block, offset) in 32 bits.
+  check(g.block_size == 0 || g.num_slots <= static_cast<int64_t>(UINT32_MAX),
+        "paged caches of more than 2^32 slots are not supported");
   for (int p = 0; p < g.n_planes; ++p) {
     job.plane[p] = g.plane[p];
     job.base[p] = g.base[p];
