@@ -52,8 +52,23 @@ template <typename T, bool NT> __device__ __forceinline__ T ld(const T *p) {
   if constexpr (NT && LMC_KV_NT_LOADS) return __builtin_nontemporal_load(p);
   else return *p;
 }
+typedef __attribute__((address_space(1))) u32x4 GlobalU32x4;
+
+#ifndef LMC_KV_WT_STORES
+#define LMC_KV_WT_STORES 1        // device-scope write-through 16-byte stores
+#endif
+
+// Stores of HBM-only copies.  A 16-byte store is issued at device (agent)
+// scope, which writes through the XCD's L2 instead of leaving the line dirty
+// there: the kernel's end-of-launch L2 write-back then has nothing left to
+// flush, which shortens every launch (MI355X, one 256-token Llama-3-8B chunk
+// per launch: 14.4 -> 13.3 us for a 64 MiB read + write copy).  Narrower
+// vectors keep the streaming hint.
 template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
-  if constexpr (NT && LMC_KV_NT_STORES) __builtin_nontemporal_store(v, p);
+  if constexpr (NT && LMC_KV_WT_STORES && sizeof(T) == 16)
+    __builtin_amdgcn_global_store_b128((GlobalU32x4 *)(p),
+                                       __builtin_bit_cast(u32x4, v), "agent");
+  else if constexpr (NT && LMC_KV_NT_STORES) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
 
