@@ -83,12 +83,9 @@ def time_events(torch, stream, fn, iters):
     return statistics.median(ms), statistics.mean(ms), ms
 
 
-def cpu_baseline(budget_s=10.0):
-    """The oracle's numpy gather/scatter (one thread) on a bounded sample of
-    the same workload: the same 16 chunks x 32 layers x 2 planes x 2 KiB
-    rows, against a 64-block-per-layer host pool (the full 32 GiB pool does
-    not fit the host budget; the pool size does not change the per-row work).
-    """
+def cpu_oracle_rate(budget_s=3.0):
+    """The oracle's numpy gather/scatter (one thread) on the same sample as
+    cpu_torch_rate: GB/s of store+retrieve payload."""
     import numpy as np
 
     from oracle import kv_transfer as ok
@@ -102,28 +99,28 @@ def cpu_baseline(budget_s=10.0):
     lmc = [np.zeros(2 * L * CHUNK * W * ES, np.uint8) for _ in range(len(slots) // CHUNK)]
     payload = 0
     t0 = time.perf_counter()
-    passes = 0
     while True:
         for i, buf in enumerate(lmc):
             s = slots[i * CHUNK:(i + 1) * CHUNK]
             ok.multi_layer_kv_transfer(buf, table, s, pbs, True, False, 2, L, W, ES)
             ok.multi_layer_kv_transfer(buf, table, s, pbs, False, False, 2, L, W, ES)
             payload += 2 * (2 * L * len(s) * W * ES)
-        passes += 1
         if time.perf_counter() - t0 >= budget_s:
             break
-    dt = time.perf_counter() - t0
-    return {
-        "value": round(payload / dt / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{passes} x (store+retrieve of 16 chunks [2,32,256,1024] bf16, SEPARATE_KV) "
-                  f"against a {nb_cpu}-block/layer host pool; numpy oracle, 1 thread, {dt:.1f} s",
-    }
+    return round(payload / (time.perf_counter() - t0) / 1e9, 3)
 
 
 def cpu_model() -> str:
+    """lscpu's model name (falls back to /proc/cpuinfo)."""
+    try:
+        import subprocess
+
+        res = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20)
+        for line in res.stdout.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -134,12 +131,25 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_torch_path(torch, budget_s=3.0):
-    """The reference's CPU-style path (tools/cpu_vllm_runtime.py:352-419:
+def usable_cores() -> int:
+    """Cores this process may run on: os.cpu_count(), limited to the CPU
+    affinity set the host gives the process."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        pass
+    return max(1, n)
+
+
+def cpu_torch_rate(torch, threads, budget_s):
+    """The reference's CPU path (tools/cpu_vllm_runtime.py:352-419:
     index_select for the store, index_copy_ for the retrieve, per layer and
-    plane) on the same 16 chunks x 32 layers x 2 planes x 2 KiB rows
-    against a 64-block-per-layer host pool, with every thread torch may use
-    and with one thread."""
+    plane) on the benchmark's 16 chunks x 32 layers x 2 planes x 2 KiB rows
+    against a 64-block-per-layer host pool (the full 32 GiB pool does not fit
+    the host; the pool size does not change the per-row work), with
+    `threads` torch threads.  Returns (GB/s of payload, tokens/s, passes,
+    seconds)."""
     g = torch.Generator().manual_seed(0)
     nb_cpu = 64
     pool = [[torch.randn((nb_cpu * BS, W), generator=g).to(torch.bfloat16) for _ in range(2)] for _ in range(L)]
@@ -159,22 +169,42 @@ def cpu_torch_path(torch, budget_s=3.0):
                     pool[l][p].index_copy_(0, s, lmc[i][p, l])
         return 2 * 2 * L * len(slots) * W * ES
 
-    threads_all = torch.get_num_threads()
-    out = {"cpu_model": cpu_model(), "unit": "GB/s", "sample": "store+retrieve of 16 chunks [2,32,256,1024] bf16 "
-           "against a 64-block/layer host pool, torch index_select / index_copy_"}
-    for n in (threads_all, 1):
-        torch.set_num_threads(n)
+    before = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
         one_pass()
-        payload, t0 = 0, time.perf_counter()
+        payload, passes, t0 = 0, 0, time.perf_counter()
         while True:
             payload += one_pass()
+            passes += 1
             if time.perf_counter() - t0 >= budget_s:
                 break
         dt = time.perf_counter() - t0
-        out[f"threads_{n}"] = {"value": round(payload / dt / 1e9, 3),
-                               "tokens_per_s": round(payload / (2 * 2 * L * W * ES) / dt)}
-    torch.set_num_threads(threads_all)
-    return out
+    finally:
+        torch.set_num_threads(before)
+    return round(payload / dt / 1e9, 3), round(payload / (2 * 2 * L * W * ES) / dt), passes, dt
+
+
+def cpu_baseline(torch, budget_s=10.0):
+    """The reference's CPU path (cpu_torch_rate) on every usable core, with
+    the one-thread rate and the numpy oracle's one-thread rate beside it."""
+    cores = usable_cores()
+    value, tok_s, passes, dt = cpu_torch_rate(torch, cores, budget_s)
+    one, one_tok, _, _ = cpu_torch_rate(torch, 1, min(3.0, budget_s))
+    return {
+        "value": value,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{passes} x (store+retrieve of 16 chunks [2,32,256,1024] bf16, SEPARATE_KV) against a "
+                  f"64-block/layer host pool, torch index_select / index_copy_ (tools/cpu_vllm_runtime.py "
+                  f"style), {cores} threads, {dt:.1f} s",
+        "tokens_per_s": tok_s,
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "threads_1": {"value": one, "tokens_per_s": one_tok},
+        "numpy_oracle_threads_1": {"value": cpu_oracle_rate(min(3.0, budget_s))},
+    }
 
 
 def load_traffic():
@@ -822,8 +852,7 @@ def main(argv=None):
         "modes": modes,
     }
     if not args.skip_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-        out["cpu_reference_style_path"] = cpu_torch_path(torch)
+        out["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
     print(json.dumps(out))
     return 0
 

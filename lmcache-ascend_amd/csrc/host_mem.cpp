@@ -208,7 +208,7 @@ int lmc_alloc_pinned_numa_ptr(size_t size, int32_t node, uintptr_t *out_ptr) {
     // `node` for the duration of the call.
     void *p = nullptr;
     {
-      ScopedMemPolicy bind(MPOL_BIND, std::vector<int>{node});
+      numa::ThreadNodeBinding bind(node);
       hip_check(hipHostMalloc(&p, size,
                               hipHostMallocPortable | hipHostMallocMapped |
                                   hipHostMallocNumaUser),

@@ -1,4 +1,5 @@
-// Thread memory policy (NUMA) for the host allocators.
+// NUMA placement for the host allocators.  The memory-policy syscalls are
+// issued directly, so no NUMA library is linked.
 #pragma once
 
 #include "common.h"
@@ -7,56 +8,66 @@
 #include <sys/syscall.h>
 #include <unistd.h>
 
+#include <array>
 #include <cerrno>
 #include <cstring>
 #include <string>
 #include <vector>
 
 namespace lmc {
+namespace numa {
 
-// Sets the calling thread's memory policy to `mode` over `nodes` (an empty
-// list leaves the policy alone) and restores the previous one when
-// destroyed or on restore().  The syscalls are issued directly, so no NUMA
-// library is linked.
-class ScopedMemPolicy {
+constexpr int kNodeLimit = 1024;  // node ids accepted: [0, kNodeLimit)
+using NodeMask = std::array<unsigned long, kNodeLimit / (8 * sizeof(unsigned long))>;
+
+inline NodeMask mask_of(const std::vector<int> &nodes) {
+  NodeMask m{};
+  constexpr int kBitsPerWord = 8 * sizeof(unsigned long);
+  for (int n : nodes) {
+    if (n < 0 || n >= kNodeLimit)
+      fail(LMC_ERR_RUNTIME, "NUMA node " + std::to_string(n) + " is not a valid node id (expected a non-negative "
+                            "id below " + std::to_string(kNodeLimit) + ")");
+    m[n / kBitsPerWord] |= 1UL << (n % kBitsPerWord);
+  }
+  return m;
+}
+
+// Spreads the pages later allocated for [addr, addr + len) of a shared
+// mapping round-robin over `nodes`.  For a shared-memory object the policy
+// is kept by the object itself, so it decides where the object's pages land
+// whichever process or call allocates them.
+inline void interleave_range(void *addr, size_t len, const std::vector<int> &nodes) {
+  const NodeMask m = mask_of(nodes);
+  if (syscall(SYS_mbind, addr, len, MPOL_INTERLEAVE, m.data(), kNodeLimit + 1, 0) != 0)
+    fail(LMC_ERR_RUNTIME, std::string("interleaving the shared slab over its NUMA nodes failed (mbind): ") +
+                              std::strerror(errno));
+}
+
+// Restricts the calling thread's page allocations to one node for the
+// lifetime of the object, then puts the thread's previous policy back.
+class ThreadNodeBinding {
 public:
-  ScopedMemPolicy(int mode, const std::vector<int> &nodes, bool require_default = false) {
-    if (nodes.empty()) return;
-    if (syscall(SYS_get_mempolicy, &old_mode_, old_mask_, kBits + 1, nullptr, 0) != 0)
-      fail(LMC_ERR_RUNTIME, std::string("get_mempolicy failed: ") + std::strerror(errno));
-    if (require_default && old_mode_ != MPOL_DEFAULT)
-      fail(LMC_ERR_RUNTIME,
-           "shared CPU cache NUMA interleave requires the default thread memory "
-           "policy; remove the external numactl policy");
-    unsigned long mask[kWords] = {};
-    for (int n : nodes) {
-      if (n < 0 || n >= kBits)
-        fail(LMC_ERR_RUNTIME, "NUMA nodes must be in [0, " + std::to_string(kBits) + ")");
-      mask[n / 64] |= 1UL << (n % 64);
-    }
-    if (syscall(SYS_set_mempolicy, mode, mask, kBits + 1) != 0)
-      fail(LMC_ERR_RUNTIME, std::string("set_mempolicy failed: ") + std::strerror(errno));
-    active_ = true;
+  explicit ThreadNodeBinding(int node) {
+    if (syscall(SYS_get_mempolicy, &saved_mode_, saved_.data(), kNodeLimit + 1, nullptr, 0) != 0)
+      fail(LMC_ERR_RUNTIME, std::string("reading the thread's NUMA policy failed: ") + std::strerror(errno));
+    const NodeMask m = mask_of({node});
+    if (syscall(SYS_set_mempolicy, MPOL_BIND, m.data(), kNodeLimit + 1) != 0)
+      fail(LMC_ERR_RUNTIME, "binding the thread to NUMA node " + std::to_string(node) +
+                                " failed: " + std::strerror(errno));
   }
-  ~ScopedMemPolicy() {
-    if (active_) (void)put_back();
+  ~ThreadNodeBinding() {
+    if (saved_mode_ == MPOL_DEFAULT)
+      (void)syscall(SYS_set_mempolicy, MPOL_DEFAULT, nullptr, 0);
+    else
+      (void)syscall(SYS_set_mempolicy, saved_mode_, saved_.data(), kNodeLimit + 1);
   }
-  void restore() {
-    if (active_ && put_back() != 0)
-      fail(LMC_ERR_RUNTIME, std::string("restore mempolicy failed: ") + std::strerror(errno));
-  }
+  ThreadNodeBinding(const ThreadNodeBinding &) = delete;
+  ThreadNodeBinding &operator=(const ThreadNodeBinding &) = delete;
 
 private:
-  static constexpr int kBits = 1024;
-  static constexpr int kWords = kBits / 64;
-  long put_back() {
-    active_ = false;
-    if (old_mode_ == MPOL_DEFAULT) return syscall(SYS_set_mempolicy, MPOL_DEFAULT, nullptr, 0);
-    return syscall(SYS_set_mempolicy, old_mode_, old_mask_, kBits + 1);
-  }
-  bool active_ = false;
-  int old_mode_ = MPOL_DEFAULT;
-  unsigned long old_mask_[kWords] = {};
+  int saved_mode_ = MPOL_DEFAULT;
+  NodeMask saved_{};
 };
 
+} // namespace numa
 } // namespace lmc

@@ -1,13 +1,16 @@
 """GPU parity of the sparse-graph copy (sfa_copy) and the indexer C8 packet
 transport, through the C ABI.
 
-The indexer tests are the reference's device qualification tests
-(tests/standalone/test_indexer_c8_native.py) run on the MI355X: their
-expected bytes are torch indexing of the caches (short scale tails with
-guard bytes, fixed and offset chunks, int32/int64 metadata, a registered
-host packet, two streams, mixed bf16 / int8 groups, the slot factor and the
-block permutation).  Random cases with skipped chunks, slots and sources are
-compared bit for bit with the CPU oracle (oracle/kv_transfer.py).
+Every indexer case derives its expected bytes from the CPU oracle
+(oracle/kv_transfer.py: indexer_c8_transfer), on random cache contents:
+offset and fixed chunks with int32/int64 metadata, guard bytes around every
+packet, int8 keys with float16 scales at slot factor 1 and 2 and bf16 keys,
+groups of mixed key widths with unaligned packet starts, pinned host
+packets, two streams unpacking disjoint slots, and int32 block maps.  The
+chunk sizes, the guard value 173, the slot factors and the block-end slots
+are the data the reference's qualification tests use
+(tests/standalone/test_indexer_c8_native.py).  Random cases with skipped
+chunks, slots and sources are compared bit for bit with the oracle too.
 """
 
 from __future__ import annotations
@@ -34,227 +37,305 @@ def c_ops():
 
 
 # ---------------------------------------------------------------------------
-# indexer C8: the reference's qualification tests
+# indexer C8: packets, groups, pinned packets, streams and block maps, each
+# checked byte for byte against oracle.indexer_c8_transfer
 # ---------------------------------------------------------------------------
 
+GUARD, PAD = 173, 32
 
-@pytest.mark.parametrize("strided_slots", [False, True])
+
+def _c8_cache(rng, blocks, kind, slot_factor=1):
+    """Random cache contents for one layer on the CPU: int8 keys with
+    float16 scales ([blocks * slot_factor, 128, 1, 128/1]) or bf16 keys."""
+    if kind == "int8":
+        nb = blocks * slot_factor
+        keys = torch.from_numpy(rng.integers(-128, 128, size=(nb, 128, 1, 128), dtype=np.int8))
+        scales = torch.from_numpy(rng.integers(0, 0x7BFF, size=(nb, 128, 1, 1), dtype=np.uint16).view(np.float16))
+        return keys, scales
+    keys = torch.from_numpy(rng.integers(0, 1 << 16, size=(blocks, 128, 1, 128), dtype=np.uint16).view(np.int16))
+    return keys.view(torch.bfloat16), None
+
+
+def _oracle_layer(keys, scales, slot_factor=1, block_map=None):
+    return ok.C8Layer(to_bytes(keys), to_bytes(scales) if scales is not None else None, 128 * keys.element_size(),
+                      slot_factor, None if block_map is None else block_map.numpy().astype(np.int64),
+                      keys.numel() // 128 // slot_factor)
+
+
+def _packet_bytes(layer: ok.C8Layer, n: int) -> int:
+    return n * (layer.key_bytes + (2 if layer.scales is not None else 0))
+
+
+class _Packets:
+    """Packets of one layer, each inside PAD guard bytes of its own device
+    (or pinned host) buffer."""
+
+    def __init__(self, sizes, host=False):
+        self.sizes = sizes
+        self.bufs = []
+        for n in sizes:
+            if host:
+                b = torch.full((n + 2 * PAD,), GUARD, dtype=torch.uint8).pin_memory()
+            else:
+                b = torch.full((n + 2 * PAD,), GUARD, dtype=torch.uint8, device=DEV)
+            self.bufs.append(b)
+
+    def pointers(self, c_ops, host=False):
+        out = []
+        for b, n in zip(self.bufs, self.sizes):
+            out.append(c_ops.get_device_ptr(b.data_ptr() + PAD, max(n, 1)) if host else b.data_ptr() + PAD)
+        return out
+
+    def inner(self):
+        return [b.cpu().numpy()[PAD: PAD + n].copy() for b, n in zip(self.bufs, self.sizes)]
+
+    def guards_intact(self):
+        return all((b.cpu().numpy()[:PAD] == GUARD).all() and (b.cpu().numpy()[PAD + n:] == GUARD).all()
+                   for b, n in zip(self.bufs, self.sizes))
+
+    def fill(self, arrays):
+        for b, a in zip(self.bufs, arrays):
+            b[PAD: PAD + a.size].copy_(torch.from_numpy(a))
+
+
+def _chunks(counts, fixed, capacity):
+    if fixed:
+        return [c * capacity for c in range(len(counts))], counts
+    return list(np.cumsum([0] + counts[:-1])), counts
+
+
+@pytest.mark.parametrize("kind,slot_factor", [("int8", 1), ("int8", 2), ("bf16", 1)])
 @pytest.mark.parametrize("fixed", [False, True])
 @pytest.mark.parametrize("metadata_dtype", [torch.int32, torch.int64])
-def test_c8_packets_round_trip_with_short_scales(c_ops, strided_slots, fixed, metadata_dtype):
+def test_c8_pack_unpack_vs_oracle(c_ops, kind, slot_factor, fixed, metadata_dtype):
+    """Chunked packets (offset chunks of 1..1024 tokens, or fixed 1024-token
+    chunks with a short last one), guard bytes around every packet, then an
+    unpack into a cleared cache: every byte of packets and cache equals the
+    oracle's."""
+    rng = np.random.default_rng(17 + slot_factor * 3 + fixed * 5 + (metadata_dtype == torch.int64))
+    capacity = 1024
     counts = [1024, 1024, 7] if fixed else [1, 7, 127, 128, 129, 754, 1024]
     tokens = sum(counts)
-    slots = torch.arange(tokens, dtype=torch.int64) * (2 if strided_slots else 1)
-    blocks = (int(slots[-1]) + 128) // 128
-    keys_cpu = torch.arange(blocks * 128 * 128).to(torch.int8).reshape(blocks, 128, 1, 128)
-    scales_cpu = ((torch.arange(blocks * 128, dtype=torch.int32) * 97).to(torch.int16).view(torch.float16)
-                  .reshape(blocks, 128, 1, 1))
-    keys, scales = keys_cpu.to(DEV), scales_cpu.to(DEV)
-    state = c_ops.IndexerC8State(keys, scales)
-    buffers = [torch.full((130 * n + 64,), 173, dtype=torch.uint8, device=DEV) for n in counts]
-    ptrs = torch.tensor([b.data_ptr() + 32 for b in buffers], dtype=torch.int64, device=DEV)
-    lengths = torch.tensor(counts, dtype=metadata_dtype, device=DEV)
-    starts = torch.tensor([0, *torch.tensor(counts).cumsum(0).tolist()[:-1]], dtype=metadata_dtype, device=DEV)
-    slot_map = slots.to(device=DEV, dtype=metadata_dtype)
-    if fixed:
-        starts = lengths = torch.empty(1, dtype=metadata_dtype, device=DEV)
-    c_ops.indexer_c8_transfer_prepared(state, ptrs, starts, lengths, slot_map, 1024, True, fixed_chunks=fixed)
+    blocks = (tokens + 255) // 128
+    keys, scales = _c8_cache(rng, blocks, kind, slot_factor)
+    slots = rng.permutation(blocks * 128)[:tokens].astype(np.int64)
+    layer = _oracle_layer(keys, scales, slot_factor)
+    starts, lens = _chunks(counts, fixed, capacity)
+    pk = _Packets([_packet_bytes(layer, n) for n in counts])
+    state = c_ops.IndexerC8State(keys.to(DEV), scales.to(DEV) if scales is not None else None, slot_factor)
+    meta_starts = torch.tensor(starts, dtype=metadata_dtype, device=DEV)
+    meta_lens = torch.tensor(lens, dtype=metadata_dtype, device=DEV)
+    ptrs = torch.tensor(pk.pointers(c_ops), dtype=torch.int64, device=DEV)
+    slot_t = torch.from_numpy(slots).to(device=DEV, dtype=metadata_dtype)
+    c_ops.indexer_c8_transfer_prepared(state, ptrs, meta_starts, meta_lens, slot_t, capacity, True,
+                                       fixed_chunks=fixed)
+    want = [np.full(n, GUARD, np.uint8) for n in pk.sizes]
+    ok.indexer_c8_transfer([layer], [want], starts, lens, slots, capacity, True, fixed)
     torch.cuda.synchronize()
-    offset = 0
-    for n, buffer in zip(counts, buffers):
-        selected = slots[offset: offset + n]
-        expected = torch.cat((keys_cpu.view(-1, 128)[selected].contiguous().view(torch.uint8).flatten(),
-                              scales_cpu.view(-1, 1)[selected].contiguous().view(torch.uint8).flatten()))
-        actual = buffer.cpu()
-        assert torch.equal(actual[32:-32], expected)
-        assert torch.all(actual[:32] == 173) and torch.all(actual[-32:] == 173)
-        offset += n
-    keys.fill_(42)
-    scales.fill_(-1)
-    c_ops.indexer_c8_transfer_prepared(state, ptrs, starts, lengths, slot_map, 1024, False, fixed_chunks=fixed)
-    actual_keys, actual_scales = keys.cpu().view(-1, 128), scales.cpu().view(-1, 1)
-    assert torch.equal(actual_keys[slots], keys_cpu.view(-1, 128)[slots])
-    assert torch.equal(actual_scales.view(torch.int16)[slots], scales_cpu.view(-1, 1).view(torch.int16)[slots])
-    untouched = torch.ones(blocks * 128, dtype=torch.bool)
-    untouched[slots] = False
-    assert torch.all(actual_keys[untouched] == 42)
-    assert torch.all(actual_scales[untouched] == -1)
+    for got, w in zip(pk.inner(), want):
+        assert np.array_equal(got, w)
+    assert pk.guards_intact()
+    # unpack into a cleared cache
+    state.keys.fill_(42)
+    if state.scales is not None:
+        state.scales.view(torch.int16).fill_(-1)
+    cleared = _oracle_layer(state.keys.cpu(), state.scales.cpu() if state.scales is not None else None, slot_factor)
+    c_ops.indexer_c8_transfer_prepared(state, ptrs, meta_starts, meta_lens, slot_t, capacity, False,
+                                       fixed_chunks=fixed)
+    ok.indexer_c8_transfer([cleared], [want], starts, lens, slots, capacity, False, fixed)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bytes(state.keys), cleared.keys)
+    if state.scales is not None:
+        assert np.array_equal(to_bytes(state.scales), cleared.scales)
 
 
-def test_c8_rejects_wrong_scale_dtype_and_metadata(c_ops):
-    keys = torch.empty(2, 128, 1, 128, dtype=torch.int8, device=DEV)
-    scales = torch.empty(2, 128, 1, 1, dtype=torch.float16, device=DEV)
-    with pytest.raises(RuntimeError, match="float16 scales"):
-        c_ops.IndexerC8State(keys, scales.bfloat16())
-    state = c_ops.IndexerC8State(keys, scales)
-    meta = torch.empty(0, dtype=torch.int64, device=DEV)
-    with pytest.raises(RuntimeError, match="int32/int64 vectors"):
-        c_ops.indexer_c8_transfer_prepared(state, meta.cpu(), meta, meta, meta, 1024, False)
-    with pytest.raises(RuntimeError, match="PA_BSND"):
-        c_ops.IndexerC8State(torch.empty(2, 64, 1, 128, dtype=torch.bfloat16, device=DEV))
-    with pytest.raises(RuntimeError, match="block factor"):
-        c_ops.IndexerC8State(torch.empty(2, 128, 1, 128, dtype=torch.bfloat16, device=DEV), None, 2)
-
-
-@pytest.mark.parametrize("layers", [1, 3])
-def test_c8_group_keeps_layers_and_planes_separate(c_ops, layers):
-    keys = [torch.full((2, 128, 1, 128), i + 1, dtype=torch.int8, device=DEV) for i in range(layers)]
-    scales = [torch.full((2, 128, 1, 1), (i + 1) / 16, dtype=torch.float16, device=DEV) for i in range(layers)]
-    state = c_ops.IndexerC8GroupState([c_ops.IndexerC8State(k, s) for k, s in zip(keys, scales)])
-    # Adjacent layer packets have unaligned starts after layer 0.
-    packet = torch.full((layers * 7 * 130,), 255, dtype=torch.uint8, device=DEV)
-    pointers = torch.tensor([[packet.data_ptr() + i * 7 * 130] for i in range(layers)], dtype=torch.int64,
-                            device=DEV)
-    offsets = torch.tensor([0], dtype=torch.int32, device=DEV)
-    counts = torch.tensor([7], dtype=torch.int32, device=DEV)
-    slots = torch.arange(7, dtype=torch.int64, device=DEV)
-    c_ops.indexer_c8_group_transfer_prepared(state, pointers, offsets, counts, slots, 7, True)
-    actual = packet.cpu().view(layers, 7 * 130)
-    for i in range(layers):
-        assert torch.all(actual[i, : 7 * 128].view(torch.int8) == i + 1)
-        assert torch.all(actual[i, 7 * 128:].view(torch.float16) == (i + 1) / 16)
+@pytest.mark.parametrize("kinds", [["int8"], ["bf16", "int8", "int8"], ["int8", "bf16"]])
+@pytest.mark.parametrize("slot_factor", [1, 2])
+def test_c8_group_vs_oracle(c_ops, kinds, slot_factor):
+    """One launch over several layers of different key widths.  Each layer's
+    packets sit back to back in one buffer, so every layer after the first
+    starts at an address that is not 16-byte aligned."""
+    rng = np.random.default_rng(len(kinds) * 10 + slot_factor)
+    blocks, capacity = 6, 300
+    counts = [300, 41, 259]
+    starts = [0, 300, 341]
+    tokens = sum(counts)
+    slots = rng.permutation(blocks * 128)[:tokens].astype(np.int64)
+    caches, layers = [], []
+    for kd in kinds:
+        sf = slot_factor if kd == "int8" else 1
+        k, s = _c8_cache(rng, blocks, kd, sf)
+        caches.append((k.to(DEV), s.to(DEV) if s is not None else None, sf))
+        layers.append(_oracle_layer(k, s, sf))
+    state = c_ops.IndexerC8GroupState([c_ops.IndexerC8State(k, s, sf) for k, s, sf in caches])
+    sizes = [[_packet_bytes(L, n) for n in counts] for L in layers]
+    total = sum(sum(x) for x in sizes)
+    buf = torch.full((total + 2 * PAD,), GUARD, dtype=torch.uint8, device=DEV)
+    ptr_rows, pos = [], PAD
+    for row in sizes:
+        ptr_rows.append([])
+        for n in row:
+            ptr_rows[-1].append(buf.data_ptr() + pos)
+            pos += n
+    ptrs = torch.tensor(ptr_rows, dtype=torch.int64, device=DEV)
+    offs = torch.tensor(starts, dtype=torch.int32, device=DEV)
+    cnts = torch.tensor(counts, dtype=torch.int32, device=DEV)
+    slot_t = torch.from_numpy(slots).to(DEV)
+    c_ops.indexer_c8_group_transfer_prepared(state, ptrs, offs, cnts, slot_t, capacity, True)
+    want = [[np.full(n, GUARD, np.uint8) for n in row] for row in sizes]
+    ok.indexer_c8_transfer(layers, want, starts, counts, slots, capacity, True, False)
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[PAD: PAD + total], np.concatenate([w for row in want for w in row]))
+    assert (got[:PAD] == GUARD).all() and (got[PAD + total:] == GUARD).all()
+    # unpack every layer into cleared caches
+    for k, s, _ in caches:
+        k.view(torch.uint8).fill_(9)
+        if s is not None:
+            s.view(torch.uint8).fill_(9)
+    cleared = [_oracle_layer(k.cpu(), s.cpu() if s is not None else None, sf) for k, s, sf in caches]
+    c_ops.indexer_c8_group_transfer_prepared(state, ptrs, offs, cnts, slot_t, capacity, False)
+    ok.indexer_c8_transfer(cleared, want, starts, counts, slots, capacity, False, False)
+    torch.cuda.synchronize()
+    for (k, s, _), L in zip(caches, cleared):
+        assert np.array_equal(to_bytes(k), L.keys)
+        if s is not None:
+            assert np.array_equal(to_bytes(s), L.scales)
 
 
 @pytest.mark.parametrize("tokens", [1, 7, 129])
-def test_c8_registered_cpu_packet_round_trip(c_ops, tokens):
-    keys = torch.arange(4 * 128 * 128).to(torch.int8).reshape(4, 128, 1, 128).to(DEV)
-    scales = ((torch.arange(4 * 128, dtype=torch.int32) * 97).to(torch.int16).view(torch.float16)
-              .reshape(4, 128, 1, 1).to(DEV))
-    state = c_ops.IndexerC8State(keys, scales)
-    slots_cpu = torch.arange(tokens, dtype=torch.int64) * 2
-    slots = slots_cpu.to(DEV)
-    expected_keys = keys.cpu().view(-1, 128)[slots_cpu]
-    expected_scales = scales.cpu().view(-1, 1)[slots_cpu]
-    payload = torch.cat((expected_keys.contiguous().view(torch.uint8).flatten(),
-                         expected_scales.contiguous().view(torch.uint8).flatten()))
-    allocation = int(c_ops.alloc_pinned_ptr(tokens * 130 + 64, 0))
+def test_c8_pinned_host_packet_vs_oracle(c_ops, tokens):
+    """A packet in pinned host memory (alloc_pinned_ptr), addressed through
+    get_device_ptr: packed and unpacked over PCIe."""
+    rng = np.random.default_rng(tokens)
+    keys, scales = _c8_cache(rng, 4, "int8")
+    layer = _oracle_layer(keys, scales)
+    slots = rng.permutation(4 * 128)[:tokens].astype(np.int64)
+    n = _packet_bytes(layer, tokens)
+    alloc = int(c_ops.alloc_pinned_ptr(n + 2 * PAD, 0))
     try:
-        ctypes.memset(allocation, 173, tokens * 130 + 64)
-        device_pointer = int(c_ops.get_device_ptr(allocation + 32, tokens * 130))
-        assert device_pointer
-        pointers = torch.tensor([device_pointer], dtype=torch.int64, device=DEV)
-        offsets = torch.tensor([0], dtype=torch.int32, device=DEV)
-        counts = torch.tensor([tokens], dtype=torch.int32, device=DEV)
-        c_ops.indexer_c8_transfer_prepared(state, pointers, offsets, counts, slots, tokens, True)
+        ctypes.memset(alloc, GUARD, n + 2 * PAD)
+        dev_ptr = int(c_ops.get_device_ptr(alloc + PAD, n))
+        assert dev_ptr
+        state = c_ops.IndexerC8State(keys.to(DEV), scales.to(DEV))
+        args = (torch.tensor([dev_ptr], dtype=torch.int64, device=DEV), torch.tensor([0], dtype=torch.int32, device=DEV),
+                torch.tensor([tokens], dtype=torch.int32, device=DEV), torch.from_numpy(slots).to(DEV), tokens)
+        c_ops.indexer_c8_transfer_prepared(state, *args, True)
+        want = np.full(n, GUARD, np.uint8)
+        ok.indexer_c8_transfer([layer], [[want]], [0], [tokens], slots, tokens, True, False)
         torch.cuda.synchronize()
-        assert ctypes.string_at(allocation + 32, tokens * 130) == payload.numpy().tobytes()
-        assert ctypes.string_at(allocation, 32) == bytes([173]) * 32
-        assert ctypes.string_at(allocation + 32 + tokens * 130, 32) == bytes([173]) * 32
-        keys.zero_()
-        scales.zero_()
-        c_ops.indexer_c8_transfer_prepared(state, pointers, offsets, counts, slots, tokens, False)
+        host = np.frombuffer(ctypes.string_at(alloc, n + 2 * PAD), dtype=np.uint8)
+        assert np.array_equal(host[PAD: PAD + n], want)
+        assert (host[:PAD] == GUARD).all() and (host[PAD + n:] == GUARD).all()
+        state.keys.zero_()
+        state.scales.zero_()
+        cleared = _oracle_layer(state.keys.cpu(), state.scales.cpu())
+        c_ops.indexer_c8_transfer_prepared(state, *args, False)
+        ok.indexer_c8_transfer([cleared], [[want]], [0], [tokens], slots, tokens, False, False)
         torch.cuda.synchronize()
-        assert torch.equal(keys.cpu().view(-1, 128)[slots_cpu], expected_keys)
-        assert torch.equal(scales.cpu().view(-1, 1).view(torch.int16)[slots_cpu], expected_scales.view(torch.int16))
+        assert np.array_equal(to_bytes(state.keys), cleared.keys)
+        assert np.array_equal(to_bytes(state.scales), cleared.scales)
     finally:
         torch.cuda.synchronize()
-        c_ops.free_pinned_ptr(allocation)
+        c_ops.free_pinned_ptr(alloc)
 
 
-def test_c8_repeated_copy_on_two_streams_keeps_disjoint_slots(c_ops):
-    tokens = 257
-    keys = torch.full((5, 128, 1, 128), -7, dtype=torch.int8, device=DEV)
-    scales = torch.full((5, 128, 1, 1), -1, dtype=torch.float16, device=DEV)
-    state = c_ops.IndexerC8State(keys, scales)
+def test_c8_unpack_on_two_streams_vs_oracle(c_ops):
+    """Two streams unpack their own packets, repeatedly, into disjoint slots
+    of one cache; the result equals the oracle applying both (the slot sets
+    are disjoint, so the order of the streams does not matter)."""
+    rng = np.random.default_rng(3)
+    blocks, tokens = 5, 257
+    keys, scales = _c8_cache(rng, blocks, "int8")
+    state = c_ops.IndexerC8State(keys.to(DEV), scales.to(DEV))
+    layer = _oracle_layer(keys, scales)
+    perm = rng.permutation(blocks * 128)
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
-    owners = []
-    for rank, stream in enumerate(streams):
-        key_bits = ((torch.arange(tokens * 128) + rank * 37) % 256).to(torch.uint8)
-        scale_bits = ((torch.arange(tokens) + rank * 991) * 97).to(torch.int16)
-        packet = torch.cat((key_bits, scale_bits.view(torch.uint8))).to(DEV)
-        pointers = torch.tensor([packet.data_ptr()], dtype=torch.int64, device=DEV)
-        offsets = torch.zeros(1, dtype=torch.int32, device=DEV)
-        counts = torch.tensor([tokens], dtype=torch.int32, device=DEV)
-        slots = (torch.arange(tokens, dtype=torch.int64) * 2 + rank).to(DEV)
-        stream.wait_stream(torch.cuda.current_stream())
-        owners.append((packet, pointers, offsets, counts, slots, key_bits, scale_bits))
-        with torch.cuda.stream(stream):
+    keep = []
+    for i, st in enumerate(streams):
+        slots = perm[i * tokens: (i + 1) * tokens].astype(np.int64)
+        packet = rng.integers(0, 256, size=_packet_bytes(layer, tokens), dtype=np.uint8)
+        dev_packet = torch.from_numpy(packet).to(DEV)
+        args = (torch.tensor([dev_packet.data_ptr()], dtype=torch.int64, device=DEV),
+                torch.zeros(1, dtype=torch.int32, device=DEV), torch.tensor([tokens], dtype=torch.int32, device=DEV),
+                torch.from_numpy(slots).to(DEV), tokens)
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
             for _ in range(16):
-                c_ops.indexer_c8_transfer_prepared(state, pointers, offsets, counts, slots, tokens, False)
+                c_ops.indexer_c8_transfer_prepared(state, *args, False)
+        keep.append((dev_packet, args))
+        ok.indexer_c8_transfer([layer], [[packet]], [0], [tokens], slots, tokens, False, False)
     torch.cuda.synchronize()
-    key_result = keys.cpu().view(-1, 128).view(torch.uint8)
-    scale_result = scales.cpu().view(-1).view(torch.int16)
-    for _, _, _, _, slots, expected_keys, expected_scales in owners:
-        indices = slots.cpu()
-        assert torch.equal(key_result[indices].flatten(), expected_keys)
-        assert torch.equal(scale_result[indices], expected_scales)
-    assert torch.all(keys.cpu().view(-1, 128)[tokens * 2:] == -7)
-    assert torch.all(scales.cpu().view(-1)[tokens * 2:] == -1)
-
-
-@pytest.mark.parametrize("slot_factor", [1, 2])
-def test_c8_mixed_group_preserves_bf16_bits_and_c8_physical_mapping(c_ops, slot_factor):
-    tokens = 259
-    bf16_cpu = torch.arange(4 * 128 * 128).to(torch.int16).view(torch.bfloat16).reshape(4, 128, 1, 128)
-    c8_cpu = torch.arange(4 * slot_factor * 128 * 128).to(torch.int8).reshape(4 * slot_factor, 128, 1, 128)
-    scale_cpu = ((torch.arange(4 * slot_factor * 128) * 97).to(torch.int16).view(torch.float16)
-                 .reshape(4 * slot_factor, 128, 1, 1))
-    bf16, c8, scale = bf16_cpu.to(DEV), c8_cpu.to(DEV), scale_cpu.to(DEV)
-    state = c_ops.IndexerC8GroupState([c_ops.IndexerC8State(bf16), c_ops.IndexerC8State(c8, scale, slot_factor)])
-    packets = [torch.empty(tokens * width, dtype=torch.uint8, device=DEV) for width in (256, 130)]
-    pointers = torch.tensor([[p.data_ptr()] for p in packets], dtype=torch.int64, device=DEV)
-    offsets = torch.tensor([0], dtype=torch.int32, device=DEV)
-    sizes = torch.tensor([tokens], dtype=torch.int32, device=DEV)
-    slots = torch.arange(tokens, dtype=torch.int64, device=DEV)
-    physical = torch.arange(tokens) + (torch.arange(tokens) // 128) * (slot_factor - 1) * 128
-    c_ops.indexer_c8_group_transfer_prepared(state, pointers, offsets, sizes, slots, tokens, True)
-    expected_bf16 = bf16_cpu.view(-1, 128)[:tokens].contiguous().view(torch.uint8).flatten()
-    expected_c8 = torch.cat((c8_cpu.view(-1, 128)[physical].contiguous().view(torch.uint8).flatten(),
-                             scale_cpu.view(-1, 1)[physical].contiguous().view(torch.uint8).flatten()))
-    assert torch.equal(packets[0].cpu(), expected_bf16)
-    assert torch.equal(packets[1].cpu(), expected_c8)
-    bf16.zero_()
-    c8.zero_()
-    scale.zero_()
-    c_ops.indexer_c8_group_transfer_prepared(state, pointers, offsets, sizes, slots, tokens, False)
-    assert torch.equal(bf16.cpu().view(-1, 128)[:tokens].contiguous().view(torch.uint8).flatten(), expected_bf16)
-    assert torch.equal(c8.cpu().view(-1, 128)[physical], c8_cpu.view(-1, 128)[physical])
-    assert torch.equal(scale.cpu().view(torch.int16).view(-1)[physical],
-                       scale_cpu.view(torch.int16).view(-1)[physical])
+    assert np.array_equal(to_bytes(state.keys), layer.keys)
+    assert np.array_equal(to_bytes(state.scales), layer.scales)
 
 
 @pytest.mark.parametrize("grouped", [False, True])
-def test_c8_paired_bank_copy_roundtrip_and_unused_rows(c_ops, grouped):
+def test_c8_block_map_vs_oracle(c_ops, grouped):
+    """An int32 block map sends logical block b to physical block map[b];
+    the selected slots straddle block ends (offsets 126..128), alone and
+    behind a bf16 layer in a group."""
     assert getattr(c_ops, "INDEXER_C8_BLOCK_MAP_ABI", 0) >= 1
-    t = 3
-    mapping = torch.empty(18 * t, dtype=torch.int32)
-    for u in range(t):
-        ids = [*range(8 * u, 8 * u + 8), *range(8 * (t + u), 8 * (t + u) + 8), 16 * t + u, 17 * t + u]
-        mapping[ids] = torch.tensor([*range(16 * u, 16 * u + 16), 16 * t + 2 * u, 16 * t + 2 * u + 1],
-                                    dtype=torch.int32)
-    keys = torch.arange(18 * t * 128 * 128).to(torch.int8).reshape(18 * t, 128, 1, 128).to(DEV)
-    scales = ((torch.arange(18 * t * 128) * 97).to(torch.int16).view(torch.float16)
-              .reshape(18 * t, 128, 1, 1).to(DEV))
-    state = c_ops.IndexerC8State(keys, scales, 1, mapping.to(DEV))
-    host_slots = torch.cat([torch.arange(b * 128 + 126, b * 128 + 129) for b in (23, 47, 50)])
-    physical = mapping[host_slots // 128].long() * 128 + host_slots % 128
-    expected = torch.cat([keys.cpu().view(-1, 128)[physical].contiguous().view(torch.uint8).flatten(),
-                          scales.cpu().view(-1)[physical].contiguous().view(torch.uint8).flatten()])
-    packet = torch.zeros_like(expected, device=DEV)
-    ptr = torch.tensor([packet.data_ptr()], dtype=torch.int64, device=DEV)
-    offsets = torch.tensor([0], dtype=torch.int32, device=DEV)
-    counts = torch.tensor([len(host_slots)], dtype=torch.int32, device=DEV)
-    slots = host_slots.to(DEV)
+    rng = np.random.default_rng(11 + grouped)
+    blocks = 54
+    keys, scales = _c8_cache(rng, blocks, "int8")
+    block_map = torch.from_numpy(rng.permutation(blocks).astype(np.int32))
+    slots = np.concatenate([np.arange(b * 128 + 126, b * 128 + 129) for b in (23, 47, 50)]).astype(np.int64)
+    n = len(slots)
+    c8 = c_ops.IndexerC8State(keys.to(DEV), scales.to(DEV), 1, block_map.to(DEV))
+    layers = [_oracle_layer(keys, scales, 1, block_map)]
+    states = [c8]
     if grouped:
-        bf = torch.full_like(keys, 5, dtype=torch.bfloat16)
-        bf_packet = torch.empty(len(host_slots) * 256, dtype=torch.uint8, device=DEV)
-        state = c_ops.IndexerC8GroupState([c_ops.IndexerC8State(bf), state])
-        ptr = torch.tensor([[bf_packet.data_ptr()], [packet.data_ptr()]], dtype=torch.int64, device=DEV)
-    fn = c_ops.indexer_c8_group_transfer_prepared if grouped else c_ops.indexer_c8_transfer_prepared
-    fn(state, ptr, offsets, counts, slots, len(host_slots), True)
+        bf_keys, _ = _c8_cache(rng, blocks, "bf16")
+        states.insert(0, c_ops.IndexerC8State(bf_keys.to(DEV)))
+        layers.insert(0, _oracle_layer(bf_keys, None))
+    packets = [torch.zeros(_packet_bytes(L, n), dtype=torch.uint8, device=DEV) for L in layers]
+    args = (torch.tensor([[p.data_ptr()] for p in packets], dtype=torch.int64, device=DEV) if grouped else
+            torch.tensor([packets[0].data_ptr()], dtype=torch.int64, device=DEV),
+            torch.tensor([0], dtype=torch.int32, device=DEV), torch.tensor([n], dtype=torch.int32, device=DEV),
+            torch.from_numpy(slots).to(DEV), n)
+    run = c_ops.indexer_c8_group_transfer_prepared if grouped else c_ops.indexer_c8_transfer_prepared
+    state = c_ops.IndexerC8GroupState(states) if grouped else c8
+    run(state, *args, True)
+    want = [[np.zeros(_packet_bytes(L, n), np.uint8)] for L in layers]
+    ok.indexer_c8_transfer(layers, want, [0], [n], slots, n, True, False)
     torch.cuda.synchronize()
-    assert torch.equal(packet.cpu(), expected)
-    keys.zero_()
-    scales.zero_()
-    fn(state, ptr, offsets, counts, slots, len(host_slots), False)
+    for p, w in zip(packets, want):
+        assert np.array_equal(to_bytes(p), w[0])
+    for st in states:
+        st.keys.zero_()
+        if st.scales is not None:
+            st.scales.zero_()
+    cleared = [_oracle_layer(st.keys.cpu(), st.scales.cpu() if st.scales is not None else None, 1,
+                             st.block_map.cpu() if st.block_map is not None else None) for st in states]
+    run(state, *args, False)
+    ok.indexer_c8_transfer(cleared, want, [0], [n], slots, n, False, False)
     torch.cuda.synchronize()
-    actual = torch.cat([keys.cpu().view(-1, 128)[physical].contiguous().view(torch.uint8).flatten(),
-                        scales.cpu().view(-1)[physical].contiguous().view(torch.uint8).flatten()])
-    assert torch.equal(actual, expected)
-    unused = torch.ones(18 * t * 128, dtype=torch.bool)
-    unused[physical] = False
-    assert keys.cpu().view(-1, 128)[unused].eq(0).all()
-    assert scales.cpu().view(-1)[unused].eq(0).all()
+    for st, L in zip(states, cleared):
+        assert np.array_equal(to_bytes(st.keys), L.keys)
+        if st.scales is not None:
+            assert np.array_equal(to_bytes(st.scales), L.scales)
+
+
+@pytest.mark.parametrize("build,message", [
+    (lambda c, d: c.IndexerC8State(torch.empty(2, 128, 1, 128, dtype=torch.int8, device=d),
+                                   torch.empty(2, 128, 1, 1, dtype=torch.bfloat16, device=d)), "float16 scales"),
+    (lambda c, d: c.IndexerC8State(torch.empty(2, 64, 1, 128, dtype=torch.bfloat16, device=d)), "PA_BSND"),
+    (lambda c, d: c.IndexerC8State(torch.empty(2, 128, 1, 128, dtype=torch.bfloat16, device=d), None, 2),
+     "block factor"),
+])
+def test_c8_state_validation(c_ops, build, message):
+    with pytest.raises(RuntimeError, match=message):
+        build(c_ops, DEV)
+
+
+def test_c8_metadata_must_be_device_vectors(c_ops):
+    keys = torch.empty(2, 128, 1, 128, dtype=torch.int8, device=DEV)
+    scales = torch.empty(2, 128, 1, 1, dtype=torch.float16, device=DEV)
+    state = c_ops.IndexerC8State(keys, scales)
+    dev_meta = torch.empty(0, dtype=torch.int64, device=DEV)
+    with pytest.raises(RuntimeError, match="int32/int64 vectors"):
+        c_ops.indexer_c8_transfer_prepared(state, dev_meta.cpu(), dev_meta, dev_meta, dev_meta, 1024, False)
 
 
 # ---------------------------------------------------------------------------
