@@ -95,6 +95,10 @@ static void oc_cdf_row(const uint32_t *count, int nb, int16_t *row) {
     }
     int l = 0;
     while (((uint64_t)count[s] << l) < n) ++l; /* ceil(log2(n / c)) */
+#ifdef OC_PLANT_FLOOR_LEN
+    /* planted mistake (tests only): floor(log2(n / c)) */
+    if (((uint64_t)count[s] << l) > n) --l;
+#endif
     if (l < 1) l = 1;
     if (l > OC_MAX_LEN) l = OC_MAX_LEN;
     len[s] = l;
@@ -104,7 +108,12 @@ static void oc_cdf_row(const uint32_t *count, int nb, int16_t *row) {
     int pick = -1;
     for (int s = 0; s < nb; ++s) {
       if (len[s] == 0 || len[s] >= OC_MAX_LEN) continue;
+#ifdef OC_PLANT_TIE_LOW
+      /* planted mistake (tests only): ties pick the lowest symbol */
+      if (pick < 0 || count[s] < count[pick]) pick = s;
+#else
       if (pick < 0 || count[s] <= count[pick]) pick = s;
+#endif
     }
     if (pick < 0) break; /* unreachable: nb * 2^-12 <= 1 for nb <= 4096 */
     kraft -= (uint64_t)1 << (OC_PREC - len[pick] - 1);

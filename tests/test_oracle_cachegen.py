@@ -7,9 +7,16 @@ Checks, in order of strength:
     closed-form decode with low-bit lengths and prefix sums (:164-239);
   * closed forms of calculate_cdf: a uniform 2^n histogram gives exactly the
     reference decode test's CDF; a dyadic histogram gives the optimal code;
-  * an independent Python restatement of the CDF rule on small inputs;
+  * the defining properties of Shannon code lengths, checked on random
+    histograms: no symbol's interval exceeds its frequency share, and one
+    bit less would, wherever the alignment step did not shorten it;
+  * an independent Python restatement of the CDF rule, on small inputs and
+    on a constructed 65536-token case where the Kraft repair runs;
   * structural invariants (prefix-free, aligned, Kraft <= 1) and round trips;
-  * a planted bit-order mistake in the oracle must fail the encode KAT.
+  * planted mistakes built into the oracle: LSB-first bit packing must fail
+    the encode KAT, floor instead of ceil code lengths must fail the share
+    bound, and the other Kraft-repair tie rule fails only the repair case
+    (no chunk of at most 4096 tokens can tell the two tie rules apart).
 """
 
 import os
@@ -232,3 +239,140 @@ def test_planted_lsb_first_fails_reference_kat():
                 test_reference_basic_encode(1, 1, 3)
         finally:
             oc._lib = real
+
+
+# ---------------------------------------------------------------------------
+# Shannon-length properties of calculate_cdf, and planted CDF mistakes
+# ---------------------------------------------------------------------------
+
+
+def _share_and_minimality(syms, nb):
+    """Checks the defining properties of Shannon code lengths on every
+    stream of `syms` ([L, T, C]) whose T <= 4096 (no length reaches the
+    12-bit cap, so no Kraft repair runs):
+      share: a present symbol's interval is at most its frequency share,
+             2^-l <= c / n;
+      minimality: where the alignment step did not halve the interval (the
+             base is a multiple of twice the width), one bit less would
+             exceed the share: 2^-(l-1) > c / n, for l > 1.
+    Returns the number of symbols checked."""
+    cdf = oc.calculate_cdf(syms, nb).view(np.uint16)
+    L, T, C = syms.shape
+    assert T <= 4096
+    checked = 0
+    for l in range(L):
+        for c in range(C):
+            counts = np.bincount(syms[l, :, c][syms[l, :, c] < nb], minlength=nb)
+            n = int(counts.sum())
+            base, lens = _intervals(cdf[l, c])
+            for s in range(nb):
+                if counts[s] == 0:
+                    continue
+                cs, ls = int(counts[s]), lens[s]
+                assert n <= cs << ls, ("share", l, c, s)
+                width = 1 << (16 - ls)
+                if ls > 1 and base[s] % (2 * width) == 0:
+                    assert n > cs << (ls - 1), ("minimality", l, c, s)
+                checked += 1
+    return checked
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_cdf_shannon_share_bound_and_minimality(seed):
+    rng = np.random.default_rng(300 + seed)
+    nb = int(rng.choice([8, 16, 32, 64]))
+    T = int(rng.choice([17, 100, 256, 1000, 4096]))
+    p = rng.dirichlet(np.full(nb, float(rng.choice([0.1, 0.5, 2.0]))))
+    syms = rng.choice(nb, size=(2, T, 16), p=p).astype(np.uint8)
+    assert _share_and_minimality(syms, nb) > 0
+
+
+# 65536 tokens over 37 symbols: exact power-of-two counts plus six rare
+# symbols whose 13..14-bit Shannon lengths are capped at 12, which pushes
+# the Kraft sum over 1; the repair then lengthens two of several equally
+# frequent symbols, so the tie rule decides the code.
+REPAIR_CASE_COUNTS = [512, 1024, 512, 2048, 32, 12, 10, 5, 1024, 32768, 128, 16, 15, 64, 8192, 64, 256, 64, 1024,
+                      16, 16, 2048, 64, 4096, 2048, 256, 6, 256, 64, 16, 32, 64, 16, 8192, 32, 32, 512]
+
+
+def _repair_case():
+    nb = 64
+    counts = REPAIR_CASE_COUNTS + [0] * (nb - len(REPAIR_CASE_COUNTS))
+    syms = np.repeat(np.arange(nb, dtype=np.uint8), counts)
+    syms = np.random.default_rng(0).permutation(syms).reshape(1, -1, 1)
+    return syms, counts, nb
+
+
+def test_cdf_kraft_repair_case_matches_python_restatement():
+    syms, counts, nb = _repair_case()
+    cdf = oc.calculate_cdf(syms, nb).view(np.uint16)
+    assert list(cdf[0, 0]) == _py_cdf_row(counts)
+    base, lens = _intervals(cdf[0, 0])
+    assert sum(2.0 ** -ln for ln in lens if ln) <= 1.0
+
+
+def _run_checks():
+    """Every CPU check of calculate_cdf, by name -> passed?"""
+    checks = {
+        "uniform closed form": lambda: [test_cdf_of_uniform_histogram_is_reference_decode_cdf(b) for b in range(1, 7)],
+        "dyadic closed form": test_cdf_dyadic_histogram_is_optimal,
+        "single and empty": test_cdf_single_and_empty,
+        "structural invariants": lambda: [test_cdf_structural_invariants(s) for s in range(6)],
+        "round trip": lambda: [test_round_trip(s) for s in range(8)],
+        "share bound and minimality": lambda: [test_cdf_shannon_share_bound_and_minimality(s) for s in range(8)],
+        "python restatement": lambda: [test_cdf_matches_python_restatement(s) for s in range(12)],
+        "restatement on the Kraft repair case": test_cdf_kraft_repair_case_matches_python_restatement,
+    }
+    out = {}
+    for name, fn in checks.items():
+        try:
+            fn()
+            out[name] = True
+        except AssertionError:
+            out[name] = False
+    return out
+
+
+def _with_planted(flag, fn):
+    src = os.path.join(os.path.dirname(oc.__file__), "cachegen.c")
+    with tempfile.TemporaryDirectory() as d:
+        lib = os.path.join(d, "planted.so")
+        subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-D" + flag, src, "-o", lib], check=True)
+        planted = oc.load_library(lib)
+        real = oc._load()
+        try:
+            oc._lib = planted
+            return fn()
+        finally:
+            oc._lib = real
+
+
+def test_planted_floor_length_is_caught_by_the_shannon_properties():
+    """floor(log2(n/c)) instead of ceil: the closed forms (uniform, dyadic)
+    cannot see it (their shares are exact powers of two) and the Kraft
+    repair keeps every structural invariant and round trip intact; the
+    share bound catches it, as does the restatement."""
+    passed = _with_planted("OC_PLANT_FLOOR_LEN", _run_checks)
+    assert not passed["share bound and minimality"]
+    assert not passed["python restatement"]
+    for name in ("uniform closed form", "dyadic closed form", "single and empty", "structural invariants",
+                 "round trip"):
+        assert passed[name], name
+
+
+def test_planted_tie_break_is_caught_only_by_the_repair_case():
+    """Ties in the Kraft repair going to the lowest symbol instead of the
+    highest: no property can tell the two rules apart (both yield valid
+    prefix codes of equal cost), only the restatement on a case where the
+    repair runs.  The repair needs a length capped at 12 bits, i.e. more
+    than 4096 tokens, so no CDF of a chunk of at most 4096 tokens (LMCache
+    chunks hold 256) depends on the tie rule."""
+    passed = _with_planted("OC_PLANT_TIE_LOW", _run_checks)
+    assert not passed["restatement on the Kraft repair case"]
+    assert all(ok for name, ok in passed.items() if name != "restatement on the Kraft repair case"), passed
+    rng = np.random.default_rng(9)
+    syms = np.concatenate([rng.choice(32, size=(1, 4096, 64), p=rng.dirichlet(np.full(32, a))).astype(np.uint8)
+                           for a in (0.05, 0.3, 1.0)])
+    real = oc.calculate_cdf(syms, 32)
+    planted = _with_planted("OC_PLANT_TIE_LOW", lambda: oc.calculate_cdf(syms, 32))
+    assert np.array_equal(real, planted)
