@@ -663,6 +663,32 @@ def main(argv=None):
         extra["d2d_per_chunk_calls_store"] = time_events(torch, stream, store_per_chunk, 10)[0]
         extra["d2d_per_chunk_calls_retrieve"] = time_events(torch, stream, retrieve_per_chunk, 10)[0]
 
+        # Floors for one launch per memory object: the same 16 calls with the
+        # identity slots 0..4095 (each call then copies contiguous rows), and
+        # the runtime's own device copy of the same 32 MiB per call.
+        lin = torch.arange(n_tok, dtype=torch.int64, device=dev)
+
+        def identity_per_chunk(direction):
+            for x, s in zip(chunks, starts):
+                ops.multi_layer_kv_transfer(x, ptrs, lin[s: s + x.shape[2]], dev, pbs, direction, False, 2, W, W, 0)
+
+        identity_per_chunk(True)
+        extra["d2d_per_chunk_identity_slots_store"] = time_events(
+            torch, stream, lambda: identity_per_chunk(True), 10)[0]
+        extra["d2d_per_chunk_identity_slots_retrieve"] = time_events(
+            torch, stream, lambda: identity_per_chunk(False), 10)[0]
+        flat_src = torch.empty(2 * L * CHUNK * W * ES * len(chunks), dtype=torch.uint8, device=dev)
+        flat_dst = torch.empty_like(flat_src)
+        cb = 2 * L * CHUNK * W * ES
+
+        def memcpy_per_chunk():
+            for i in range(len(chunks)):
+                flat_dst[i * cb:(i + 1) * cb].copy_(flat_src[i * cb:(i + 1) * cb])
+
+        memcpy_per_chunk()
+        extra["hipmemcpy_d2d_per_chunk_32MiB"] = time_events(torch, stream, memcpy_per_chunk, 10)[0]
+        del flat_src, flat_dst
+
         # The same 16 calls captured once in a HIP graph and replayed: no host
         # work per call.
         graphs = {}

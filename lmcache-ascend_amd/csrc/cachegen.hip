@@ -28,6 +28,7 @@
 // are one coalesced 256-byte row.  Per-stream tables (histogram, code table,
 // decode table) live in LDS as [symbol][lane] so every lane works in its own
 // column without bank conflicts or barriers.
+#include <type_traits>
 #include "common.h"
 #include "cachegen_decode.h"
 
@@ -606,6 +607,9 @@ __global__ void __launch_bounds__(kEncTileThreads)
 // of L2 tables (or a prefix spans more than 16 symbols), which falls back
 // to a binary search over the bases.
 constexpr int kDecLanes = cgdec::kLanes;
+#ifndef LMC_DEC_LANES
+#define LMC_DEC_LANES 1  // per-lane stream regions for n_bins <= 32
+#endif
 constexpr int kDirectBits = 7;
 constexpr int kSubBits = 5;
 constexpr int kSubTables = 4;
@@ -1056,6 +1060,149 @@ __device__ __forceinline__ void decode_one_wave(uint8_t *lds, const int16_t *__r
   }
 }
 
+// Byte tables with per-lane stream regions (cgdec::LaneRegion): each lane
+// stages the 16-byte aligned chunks holding its own stream into its own LDS
+// region and rewrites them as big-endian dwords ending in a zero dword, so
+// the cursor (cgdec::LaneCursor, a 64-bit window refilled once per two codes
+// of at most 8 bits) reads region dwords without masking the stream's end.
+// Serves full 64-stream blocks with dword-aligned output rows whose regions
+// fit the LDS left after the tables and rows; returns false, having written
+// nothing, for any other block, which then takes decode_one_wave.
+__device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_t *__restrict__ cdf,
+                                                      const uint8_t *__restrict__ bytes, int64_t nbytes,
+                                                      const int32_t *__restrict__ prefix, int T, int C, int nb,
+                                                      uint8_t *__restrict__ out, int tiles, int lane) {
+  using Tab = cgdec::ByteTables;
+  constexpr int kRowsOff = Tab::kBytes + kObufBytes;
+  constexpr int kLaneBatch = 8;  // 16-byte chunks per lane and load batch
+  const int rows_cap = ((nb + 1) * kDecLanes * 2 + 32 + 15) & ~15;
+  const int reg_off = kRowsOff + rows_cap;
+  const uint32_t reg_cap = static_cast<uint32_t>((kDecLds - reg_off) & ~15);
+  // LDS address of the block's table (the start of the kernel's dynamic
+  // LDS); the table step ORs a dword offset into it.
+  const uint32_t lds_at =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *)lds));
+  DecBlock bk;
+  bk.init(cdf, nbytes, prefix, C, nb, tiles, lane);
+  if (bk.cnt != kDecLanes || (reinterpret_cast<uintptr_t>(out) & 3) != 0 || (C & 3) != 0 ||
+      (lds_at & (Tab::kBytes - 1)) != 0)
+    return false;
+  // The rows' loads depend on the block alone: issued before the stream
+  // lengths (prefix loads) are waited for.
+  const int nrow = static_cast<int>((bk.R1 - bk.r_lo + 15) >> 4);
+  chunk16 rv[kRowChunks], cv[kLaneBatch];
+  load_chunks(bk.r_lo, nrow, 0, lane, rv);
+  const uintptr_t base0 = reinterpret_cast<uintptr_t>(bytes);
+  const uintptr_t s_lo = base0 + static_cast<uintptr_t>(bk.start);
+  const uintptr_t s_hi = base0 + static_cast<uintptr_t>(bk.end);
+  const uint32_t len = static_cast<uint32_t>(bk.end - bk.start);
+  const uintptr_t a0 = s_lo & ~uintptr_t(15);
+  // Chunks [a0, a0 + 16 n_ch) each hold a byte of the stream, so no load
+  // leaves the buffer's pages.
+  const uint32_t n_ch = len ? static_cast<uint32_t>(((s_hi - 1) >> 4) - (s_lo >> 4) + 1) : 0u;
+  const uint32_t rbytes = 16u * n_ch + 16u;  // chunks plus 4 dwords: the zero dword and reads ahead
+  uint32_t incl = rbytes, n_max = n_ch;
+#pragma unroll
+  for (int d = 1; d < kDecLanes; d <<= 1) {
+    const uint32_t v = __shfl_up(incl, d, kDecLanes);
+    incl += lane >= d ? v : 0u;
+    const uint32_t m = __shfl_xor(n_max, d, kDecLanes);
+    n_max = m > n_max ? m : n_max;
+  }
+  const uint32_t total = __shfl(incl, kDecLanes - 1, kDecLanes);
+  if (total > reg_cap) return false;
+  uint8_t *region = lds + reg_off + (incl - rbytes);
+  Tab tb;
+  tb.bind(lds, lane, lds_at);
+  tb.clear();
+  store_chunks<false>(lds + kRowsOff, nrow, 0, lane, rv);
+  for (int j0 = kDecLanes * kRowChunks; j0 < nrow; j0 += kDecLanes * kRowChunks) {
+    load_chunks(bk.r_lo, nrow, j0, lane, rv);
+    store_chunks<false>(lds + kRowsOff, nrow, j0, lane, rv);
+  }
+  // The first batch of the lane's chunks, issued once the rows have landed
+  // (every wave of the launch loads its rows and streams at its start, so
+  // the rows, which the table build needs first, do not share the memory
+  // system with the larger streams); the table is built while the chunks
+  // are in flight.
+#pragma unroll
+  for (int u = 0; u < kLaneBatch; ++u)
+    if (static_cast<uint32_t>(u) < n_ch) cv[u] = reinterpret_cast<global_chunk16 *>(a0)[u];
+  wave_sync();
+  tb.row.r = reinterpret_cast<const int16_t *>(lds + kRowsOff + (bk.R0 - bk.r_lo)) + lane * (nb + 1);
+  tb.nb = nb;
+  tb.build(lds + Tab::kBytes + lane);  // obuf byte: scratch for skipped writes
+#pragma unroll
+  for (int u = 0; u < kLaneBatch; ++u)
+    if (static_cast<uint32_t>(u) < n_ch) reinterpret_cast<chunk16 *>(region)[u] = cv[u];
+  for (uint32_t k0 = kLaneBatch; k0 < n_max; k0 += kLaneBatch) {
+#pragma unroll
+    for (int u = 0; u < kLaneBatch; ++u)
+      if (k0 + u < n_ch) cv[u] = reinterpret_cast<global_chunk16 *>(a0)[k0 + u];
+#pragma unroll
+    for (int u = 0; u < kLaneBatch; ++u)
+      if (k0 + u < n_ch) reinterpret_cast<chunk16 *>(region)[k0 + u] = cv[u];
+  }
+  uint32_t *reg32 = reinterpret_cast<uint32_t *>(region);
+  const uint32_t n_dw = cgdec::LaneRegion::build(reg32, static_cast<uint32_t>(s_lo - a0), len);
+  cgdec::LaneCursor cur;
+  cur.start(reg32, n_dw);
+  uint8_t *obuf = lds + Tab::kBytes;
+  uint8_t *out_blk = out + static_cast<int64_t>(bk.l) * T * C + bk.c0;
+  // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
+  uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
+  const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
+  if (!__any(tb.escapes)) {
+    int t = 0;
+    for (; t + 4 <= T; t += 4) {
+      const uint32_t s0 = tb.step8(cur), s1 = tb.step8(cur);
+      cur.refill();
+      const uint32_t s2 = tb.step8(cur), s3 = tb.step8(cur);
+      cur.refill();
+      obuf[lane] = static_cast<uint8_t>(s0);
+      obuf[kDecLanes + lane] = static_cast<uint8_t>(s1);
+      obuf[2 * kDecLanes + lane] = static_cast<uint8_t>(s2);
+      obuf[3 * kDecLanes + lane] = static_cast<uint8_t>(s3);
+      wave_sync();
+      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      odst += step4;
+      wave_sync();
+    }
+    if (t < T) {
+      for (int i = 0; t + i < T; ++i) {
+        obuf[i * kDecLanes + lane] = static_cast<uint8_t>(tb.step8(cur));
+        if (i & 1) cur.refill();
+      }
+      wave_sync();
+      if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    }
+  } else {
+    tb.finish();
+    auto step = [&]() -> uint8_t {
+      int s, l;
+      tb.lookup(cur.top16(), s, l);
+      cur.consume(l);
+      cur.refill();
+      return static_cast<uint8_t>(s);
+    };
+    int t = 0;
+    for (; t + 4 <= T; t += 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = step();
+      wave_sync();
+      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      odst += step4;
+      wave_sync();
+    }
+    if (t < T) {
+      for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = step();
+      wave_sync();
+      if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    }
+  }
+  return true;
+}
+
 template <class Tab>
 __global__ void __launch_bounds__(kDecLanes)
     decode_kernel(const int16_t *__restrict__ cdf,
@@ -1063,8 +1210,13 @@ __global__ void __launch_bounds__(kDecLanes)
                   const int32_t *__restrict__ prefix, int T, int C, int nb,
                   uint8_t *__restrict__ out, int tiles) {
   extern __shared__ uint32_t lds_words[];
-  decode_one_wave<Tab>(reinterpret_cast<uint8_t *>(lds_words), cdf, bytes, nbytes, prefix, T, C,
-                       nb, out, tiles, static_cast<int>(threadIdx.x));
+  uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
+  const int lane = static_cast<int>(threadIdx.x);
+  if constexpr (std::is_same<Tab, cgdec::ByteTables>::value) {
+    if (LMC_DEC_LANES && decode_one_wave_lanes(lds, cdf, bytes, nbytes, prefix, T, C, nb, out, tiles, lane))
+      return;
+  }
+  decode_one_wave<Tab>(lds, cdf, bytes, nbytes, prefix, T, C, nb, out, tiles, lane);
 }
 
 bool contiguous(const lmc_tensor &t) {

@@ -13,7 +13,30 @@
 namespace lmc {
 namespace cgdec {
 
+#ifndef LMC_DEC_STEP_DWORD
+#define LMC_DEC_STEP_DWORD 1
+#endif
+
 constexpr int kPrec = 16;
+
+#ifdef __HIP__
+// A dword of LDS by LDS address.
+__device__ __forceinline__ uint32_t lds_dword(uint32_t at) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(static_cast<uintptr_t>(at));
+}
+#else
+// Host build of this header (tests/decode_tables_check.cpp): the table lives
+// in host memory registered by host_lds_base.
+inline const uint8_t *&host_lds_base() {
+  static const uint8_t *base = nullptr;
+  return base;
+}
+inline uint32_t lds_dword(uint32_t at) {
+  uint32_t v;
+  __builtin_memcpy(&v, host_lds_base() + at, 4);
+  return v;
+}
+#endif
 constexpr int kLanes = 64;  // streams per decode block (one wave)
 
 // Bases and lengths read straight from a staged raw CDF row.  `wrap` is the
@@ -100,6 +123,76 @@ struct BitCursor {
   }
 };
 
+// Per-lane stream regions.  A lane's stream, bytes [start, end) of the
+// concatenated stream buffer, is staged as the raw little-endian dwords of
+// the 16-byte aligned chunks that hold it (the first chunk starts at
+// start & ~15, so the stream begins `off` = start & 15 bytes in), and then
+// rewritten in place by LaneRegion::build as big-endian dwords of the stream
+// from its first byte, the bytes past its end zeroed, followed by one zero
+// dword.  A cursor over the region reads dword min(q, n_dw), so bits past
+// the stream's end read as zero without a mask on every read.
+struct LaneRegion {
+  // In place: region[0 .. n_dw) become the stream's big-endian dwords and
+  // region[n_dw] = 0; returns n_dw = ceil(len / 4).  The raw chunks must
+  // span at least off + len bytes plus one dword, so the read one dword
+  // ahead of the last output stays inside the region; output j reads raw
+  // dwords j + off / 4 and the one after it, never an earlier index than it
+  // writes, so the rewrite is safe in place.
+  static __device__ __forceinline__ uint32_t build(uint32_t *region, uint32_t off, uint32_t len) {
+    const uint32_t ph = off >> 2, r = off & 3u, n_dw = (len + 3u) >> 2;
+    uint32_t cur = region[ph];
+    for (uint32_t j = 0; j < n_dw; ++j) {
+      const uint32_t nxt = region[j + ph + 1u];
+      const uint64_t pair = (static_cast<uint64_t>(nxt) << 32) | cur;
+      uint32_t w = __builtin_bswap32(static_cast<uint32_t>(pair >> (8u * r)));
+      const uint32_t keep = len - 4u * j;  // bytes of this dword inside the stream, >= 1
+      w &= keep >= 4u ? 0xFFFFFFFFu : ~(0xFFFFFFFFu >> (8u * keep));
+      region[j] = w;
+      cur = nxt;
+    }
+    region[n_dw] = 0u;
+    return n_dw;
+  }
+};
+
+// Bit cursor over a lane region: a 64-bit window whose top `have` bits are
+// the stream's next bits (zeros past the end are real zeros), and `next`,
+// the region dword to append, read ahead.  refill() appends it when 32 bits
+// or fewer are left, so after a refill more than 32 bits are valid: two
+// codes of at most 8 bits, or one of at most 16, can be taken between
+// refills.
+struct LaneCursor {
+  const uint32_t *w;
+  uint32_t zl;    // index of the region's zero dword (= n_dw)
+  uint32_t q;     // index of the dword in `next`
+  uint64_t win;
+  int have;
+  uint32_t next;
+
+  __device__ __forceinline__ void start(const uint32_t *region, uint32_t n_dw) {
+    w = region;
+    zl = n_dw;
+    win = (static_cast<uint64_t>(w[0]) << 32) | w[1u < zl ? 1u : zl];
+    have = 64;
+    q = 2u;
+    next = w[q < zl ? q : zl];
+  }
+  __device__ __forceinline__ uint32_t top8() const { return static_cast<uint32_t>(win >> 56); }
+  __device__ __forceinline__ uint32_t top16() const { return static_cast<uint32_t>(win >> 48); }
+  __device__ __forceinline__ void consume(int n) {
+    win <<= n;
+    have -= n;
+  }
+  __device__ __forceinline__ void refill() {
+    const bool need = have <= 32;
+    const uint64_t add = static_cast<uint64_t>(next) << ((32 - have) & 63);
+    win |= need ? add : 0ull;
+    have += need ? 32 : 0;
+    q += need ? 1u : 0u;
+    next = w[q < zl ? q : zl];
+  }
+};
+
 // Byte table for n_bins <= 32: one entry per 8-bit prefix of the 16-bit
 // window (256 per stream).  An entry is (s << 3) | (len - 1) when every
 // window with that prefix decodes to symbol s of length 1..8, and kEscape
@@ -132,13 +225,18 @@ struct ByteTables {
   static constexpr uint32_t kEscape = 0xFFu;
   static constexpr int kMaxBins = 32;
 
-  uint8_t *tab;  // block table + lane * 4
+  uint8_t *tab;      // block table + lane * 4
+  uint32_t lane_at;  // LDS address of the lane's column (table address + lane * 4)
   StagedRow row;
   int nb;
   int top;       // largest power of two below nb (1 if nb <= 2)
   bool escapes;  // some scanned entry is kEscape
 
-  __device__ __forceinline__ void bind(uint8_t *lds, int lane) { tab = lds + lane * 4; }
+  // `lds_at` is the LDS address of `lds` (a multiple of kBytes).
+  __device__ __forceinline__ void bind(uint8_t *lds, int lane, uint32_t lds_at = 0) {
+    tab = lds + lane * 4;
+    lane_at = lds_at + static_cast<uint32_t>(lane) * 4u;
+  }
 
   __device__ __forceinline__ uint8_t *entry(uint32_t e) const {
     return tab + (e >> 2) * (kLanes * 4) + (e & 3u);
@@ -233,6 +331,37 @@ struct ByteTables {
     const uint32_t x = tab[((e << 6) | e) & 0x3F03u];
     cur.advance(static_cast<int>(x & 7u) + 1);
     return x;
+  }
+
+  // One symbol at a lane cursor for a table without escapes; returns the
+  // entry (symbol e >> 3, length (e & 7) + 1).  At most 8 bits are taken.
+  // One symbol at a lane cursor for a table without escapes; returns the
+  // symbol.  At most 8 bits are taken.  With LMC_DEC_STEP_DWORD the entry is
+  // taken from the dword holding entries 4 (e / 4) .. + 3, whose address
+  // needs only the window's top 6 bits, so the chain from one symbol to the
+  // next is shorter (two operations before the LDS read, a bit-field
+  // extract after it); otherwise the entry byte is read directly.
+  __device__ __forceinline__ uint32_t step8(LaneCursor &cur) const {
+    const uint32_t hi = static_cast<uint32_t>(cur.win >> 32);
+#if LMC_DEC_STEP_DWORD
+    // dword (e / 4) of the lane's column: table byte offset (e / 4) * 256 +
+    // lane * 4, with e / 4 the window's top 6 bits; the table's LDS address
+    // is a multiple of its 16 KiB size, so the offset is ORed in.
+    const uint32_t at = ((hi >> 18) & 0x3F00u) | lane_at;
+    const uint32_t d = lds_dword(at);
+    const uint32_t sh = (hi >> 21) & 0x18u;  // 8 * (e % 4)
+    // Every code takes at least one bit: that shift does not wait for the
+    // entry, the rest (length - 1) does.
+    cur.win <<= 1;
+    cur.win <<= (d >> sh) & 7u;
+    cur.have -= static_cast<int>((d >> sh) & 7u) + 1;
+    return (d >> (sh | 3u)) & 31u;
+#else
+    const uint32_t e = hi >> 24;
+    const uint32_t x = tab[((e << 6) | e) & 0x3F03u];
+    cur.consume(static_cast<int>(x & 7u) + 1);
+    return x >> 3;
+#endif
   }
 
   // Symbol and code length for the 16-bit window v.

@@ -91,7 +91,8 @@ int main(int argc, char **argv) {
     make_row(rng, nb, kind, buf.data());
     ByteTables tb;
     memset(lds, 0xA5, sizeof lds);
-    tb.bind(lds, static_cast<int>(rng() % lmc::cgdec::kLanes));
+    lmc::cgdec::host_lds_base() = lds;
+    tb.bind(lds, static_cast<int>(rng() % lmc::cgdec::kLanes), 0);
     tb.row.r = buf.data();
     tb.nb = nb;
     tb.clear();
@@ -130,6 +131,47 @@ int main(int argc, char **argv) {
                  kind, tb.escapes ? 1 : 0, k, t, got[t], want[t]);
           return 1;
         }
+      // The lane-region path: the stream's 16-byte aligned chunks of the
+      // byte buffer (foreign bytes around it) as raw little-endian dwords,
+      // plus 4 garbage dwords, rewritten in place, then decoded with the
+      // lane cursor: two codes per refill without escapes, one with.
+      {
+        const uint32_t a0 = lo & ~15u;
+        const uint32_t n_ch = len ? ((hi - 1) / 16 - lo / 16 + 1) : 0;
+        std::vector<uint32_t> region(4 * n_ch + 4);
+        for (auto &x : region) x = static_cast<uint32_t>(rng());
+        for (uint32_t i = 0; i < 16 * n_ch; ++i)
+          reinterpret_cast<uint8_t *>(region.data())[i] = win_bytes[a0 + i];
+        const uint32_t n_dw = lmc::cgdec::LaneRegion::build(region.data(), lo - a0, len);
+        lmc::cgdec::LaneCursor lc;
+        lc.start(region.data(), n_dw);
+        int t = 0;
+        if (!tb.escapes) {
+          for (; t + 2 <= T; t += 2) {
+            got[t] = static_cast<uint8_t>(tb.step8(lc));
+            got[t + 1] = static_cast<uint8_t>(tb.step8(lc));
+            lc.refill();
+          }
+          if (t < T) {
+            got[t] = static_cast<uint8_t>(tb.step8(lc));
+            lc.refill();
+          }
+        } else {
+          for (; t < T; ++t) {
+            int s, l;
+            tb.lookup(lc.top16(), s, l);
+            got[t] = static_cast<uint8_t>(s);
+            lc.consume(l);
+            lc.refill();
+          }
+        }
+        for (int u = 0; u < T; ++u)
+          if (got[u] != want[u]) {
+            printf("LANE MISMATCH row %d (nb %d, kind %d, escapes %d) stream %d token %d: got %d want %d\n", it,
+                   nb, kind, tb.escapes ? 1 : 0, k, u, got[u], want[u]);
+            return 1;
+          }
+      }
       symbols += T;
     }
   }
