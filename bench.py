@@ -282,6 +282,103 @@ def bench_rope(torch, ops, dev, stream):
                              "tokens_per_s": round(T / t * 1e3)}}
 
 
+def bench_blend(torch, ops, dev, stream, flat, slots):
+    """The CacheBlend layerwise retrieve as the reference's connector runs it
+    (lmcache_ascend/v1/npu_connector/npu_connectors.py:556-689,
+    VLLMBufferLayerwiseNPUConnector.batched_to_gpu): for each of the 32
+    layers, 16 pinned KV_2TD memory objects [2, 256, 1024] are copied into a
+    [2, 4096, 1024] load buffer on a load stream; the buffer loaded one step
+    earlier has its K re-rotated in place (rotary_embedding_k_fused, cached
+    positions 0..4095 -> 1000..5095, theta 500000); the buffer of two steps
+    earlier is scattered into the paged caches (single_layer_kv_transfer);
+    a device-wide synchronize separates the steps and two buffers ping-pong.
+    Also timed: the same work with three buffers ordered by events instead
+    of device-wide synchronizes, and each stage alone."""
+    T = slots.numel()
+    n_obj = T // CHUNK
+    host = torch.randn((L, n_obj, 2, CHUNK, W), dtype=torch.float32).to(torch.bfloat16).pin_memory()
+    bufs = [torch.empty((2, T, W), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
+    ang = torch.outer(torch.arange(8192, dtype=torch.float32, device=dev), inv)
+    cache = torch.cat((ang.cos(), ang.sin()), dim=-1).to(torch.bfloat16)
+    old = torch.arange(T, dtype=torch.int64, device=dev)
+    new = old + 1000
+    load_stream = torch.cuda.Stream(dev)
+
+    def h2d(buf, layer):
+        for c in range(n_obj):
+            buf[0][c * CHUNK:(c + 1) * CHUNK].copy_(host[layer, c, 0], non_blocking=True)
+            buf[1][c * CHUNK:(c + 1) * CHUNK].copy_(host[layer, c, 1], non_blocking=True)
+
+    def rope(buf):
+        ops.rotary_embedding_k_fused(old, new, buf[0], D, cache, True)
+
+    def scatter(buf, layer):
+        ops.single_layer_kv_transfer(buf, (flat[2 * layer], flat[2 * layer + 1]), slots, False, 2, False, False)
+
+    def reference_pattern():
+        compute, load = bufs[0], bufs[1]
+        mapping = {}
+        for layer_id in range(L + 2):
+            if layer_id > 1:
+                scatter(mapping.pop(layer_id - 2), layer_id - 2)
+            if 0 < layer_id <= L:
+                torch.cuda.synchronize()
+                compute, load = load, compute
+                rope(compute)
+                mapping[layer_id - 1] = compute
+            if layer_id < L:
+                with torch.cuda.stream(load_stream):
+                    h2d(load, layer_id)
+        torch.cuda.synchronize()
+
+    def event_pipelined():
+        loaded = [torch.cuda.Event() for _ in range(L)]
+        done = [torch.cuda.Event() for _ in range(L)]
+        for layer in range(L):
+            buf = bufs[layer % 3]
+            with torch.cuda.stream(load_stream):
+                if layer >= 3:
+                    load_stream.wait_event(done[layer - 3])
+                h2d(buf, layer)
+                loaded[layer].record(load_stream)
+            stream.wait_event(loaded[layer])
+            rope(buf)
+            scatter(buf, layer)
+            done[layer].record(stream)
+        torch.cuda.synchronize()
+
+    def wall(fn, reps=5):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        return statistics.median(ts)
+
+    t_ref = wall(reference_pattern)
+    t_evt = wall(event_pipelined)
+    with torch.cuda.stream(load_stream):
+        t_h2d = time_events(torch, load_stream, lambda: h2d(bufs[0], 0), 10)[0]
+    t_rope = time_events(torch, stream, lambda: rope(bufs[1]), 20)[0]
+    t_scatter = time_events(torch, stream, lambda: scatter(bufs[1], 0), 20)[0]
+    layer_bytes = 2 * T * W * ES
+    out = {}
+    for name, t in (("blend_layerwise_reference_pattern_32_layers", t_ref),
+                    ("blend_layerwise_event_pipelined_32_layers", t_evt)):
+        out[name] = {"ms": round(t, 4), "ms_per_layer": round(t / L, 4),
+                     "payload_GBps": round(L * layer_bytes / (t * 1e-3) / 1e9, 2),
+                     "pcie_frac": round(L * layer_bytes / (t * 1e-3) / 1e9 / PCIE_PEAK_GBS, 4)}
+    out["blend_stage_h2d_16_objects_one_layer"] = {"ms": round(t_h2d, 4),
+                                                   "payload_GBps": round(layer_bytes / (t_h2d * 1e-3) / 1e9, 2)}
+    out["blend_stage_rope_one_layer"] = {"ms": round(t_rope, 4)}
+    out["blend_stage_scatter_one_layer"] = {"ms": round(t_scatter, 4),
+                                            "hbm_GBps": round(2 * layer_bytes / (t_scatter * 1e-3) / 1e9, 1)}
+    del host, bufs
+    return out
+
+
 def bench_qwen32b_long_prefix(torch, ops, dev, stream):
     """Qwen3-32B shape: 64 layers x 8x128 bf16, block 128; one 32768-token
     request as 128 memory objects of 256 tokens; its 256 blocks drawn without
@@ -583,7 +680,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--modes", default="d2d,per_chunk,flash,call_overhead,contiguous,pinned,staged,memcpy,cachegen,rope,qwen32b,mla576,direct,dma,c8graph",
+    ap.add_argument("--modes", default="d2d,per_chunk,flash,call_overhead,contiguous,pinned,staged,memcpy,blend,cachegen,rope,qwen32b,mla576,direct,dma,c8graph",
                     help="comma list; the timed D2D step always runs")
     args = ap.parse_args(argv)
     sel = set(args.modes.split(","))
@@ -804,6 +901,8 @@ def main(argv=None):
         extra["hipmemcpy_d2h_pinned"] = time_events(
             torch, stream, lambda: host_big.copy_(big_a, non_blocking=True), 5)[0]
 
+    if "blend" in sel:
+        extra_calls.update(bench_blend(torch, ops, dev, stream, flat, slots))
     if "cachegen" in sel:
         extra_cg = bench_cachegen(torch, ops, dev, stream)
     if "rope" in sel:
