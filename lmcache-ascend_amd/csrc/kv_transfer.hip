@@ -245,14 +245,6 @@ __global__ void __launch_bounds__(kThreads)
 // 256-token chunk (the connector's per-object call) pays on its first and
 // last waves.  Chunks of a launch hold at least one token (the host drops
 // empty ones).
-template <int NP>
-__device__ __forceinline__ int64_t pick(const int64_t (&v)[NP], int p) {
-  int64_t r = v[0];
-#pragma unroll
-  for (int i = 1; i < NP; ++i) r = p == i ? v[i] : r;
-  return r;
-}
-
 #ifndef LMC_KV_LEAN_R
 #define LMC_KV_LEAN_R 1           // lean kernel: slices per wave
 #endif
@@ -276,21 +268,24 @@ __global__ void __launch_bounds__(kThreads)
   const int spr_shift = job.spr_shift;
   const int bs_shift = job.bs_shift;
   const bool page2lmc = job.page2lmc != 0;
-  int64_t base[NP], paged_off[NP], blk_stride[NP], row_pitch[NP], lmc_fixed[NP], lmc_per_t[NP],
-      layer_fixed[NP], layer_per_t[NP], tok_stride[NP];
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    base[i] = static_cast<int64_t>(job.base[i]);
-    paged_off[i] = job.plane[i].paged_off;
-    blk_stride[i] = job.plane[i].blk_stride;
-    row_pitch[i] = job.plane[i].row_pitch;
-    lmc_fixed[i] = job.plane[i].lmc_off_fixed;
-    lmc_per_t[i] = job.plane[i].lmc_off_per_t;
-    layer_fixed[i] = job.plane[i].lmc_layer_fixed;
-    layer_per_t[i] = job.plane[i].lmc_layer_per_t;
-    tok_stride[i] = job.plane[i].lmc_token_stride;
-  }
   const int p = NP == 1 ? 0 : (y >= L) + (NP == 3 ? (y >= 2 * L) : 0);
+  // The plane's descriptor fields, each selected from the NP kernel-argument
+  // values (no private array: the compiler turns a selection over one into
+  // an indexed access of per-lane scratch memory).
+  const PlaneDesc &d0 = job.plane[0];
+  const PlaneDesc &d1 = job.plane[NP > 1 ? 1 : 0];
+  const PlaneDesc &d2 = job.plane[NP > 2 ? 2 : 0];
+  auto pick = [&](int64_t v0, int64_t v1, int64_t v2) -> int64_t {
+    return NP == 1 ? v0 : NP == 2 ? (p == 1 ? v1 : v0) : (p == 2 ? v2 : p == 1 ? v1 : v0);
+  };
+  const int64_t paged_off = pick(d0.paged_off, d1.paged_off, d2.paged_off);
+  const int64_t blk_stride = pick(d0.blk_stride, d1.blk_stride, d2.blk_stride);
+  const int64_t row_pitch = pick(d0.row_pitch, d1.row_pitch, d2.row_pitch);
+  const int64_t lmc_fixed = pick(d0.lmc_off_fixed, d1.lmc_off_fixed, d2.lmc_off_fixed);
+  const int64_t lmc_per_t = pick(d0.lmc_off_per_t, d1.lmc_off_per_t, d2.lmc_off_per_t);
+  const int64_t layer_fixed = pick(d0.lmc_layer_fixed, d1.lmc_layer_fixed, d2.lmc_layer_fixed);
+  const int64_t layer_per_t = pick(d0.lmc_layer_per_t, d1.lmc_layer_per_t, d2.lmc_layer_per_t);
+  const int64_t tok_stride = pick(d0.lmc_token_stride, d1.lmc_token_stride, d2.lmc_token_stride);
   const int l = y - p * L;
   // Independent loads: the slots and the plane's paged base.
   int t[kLeanR];
@@ -304,7 +299,8 @@ __global__ void __launch_bounds__(kThreads)
   }
   const uint64_t pbase =
       TABLE ? job.table[static_cast<int64_t>(l) * job.table_ppl + p * job.idx_step]
-            : static_cast<uint64_t>(pick<NP>(base, p));
+            : pick(static_cast<int64_t>(job.base[0]), static_cast<int64_t>(job.base[NP > 1 ? 1 : 0]),
+                   static_cast<int64_t>(job.base[NP > 2 ? 2 : 0]));
   // One wait covers all of these loads: without this the compiler places the
   // range check between them and issues the table load only after the slot.
 #pragma unroll
@@ -321,11 +317,9 @@ __global__ void __launch_bounds__(kThreads)
     const int64_t blk = slot[r] >> bs_shift;
     const int64_t in_blk = slot[r] & ((int64_t(1) << bs_shift) - 1);
     const int64_t off0 = static_cast<int64_t>((item * kLeanR + r) & ((1 << spr_shift) - 1)) * kSlice;
-    uint8_t *paged = reinterpret_cast<uint8_t *>(pbase) + pick<NP>(paged_off, p) +
-                     blk * pick<NP>(blk_stride, p) + in_blk * pick<NP>(row_pitch, p) + off0;
-    uint8_t *lm = lmc + pick<NP>(lmc_fixed, p) + pick<NP>(lmc_per_t, p) * T +
-                  static_cast<int64_t>(l) * (pick<NP>(layer_fixed, p) + pick<NP>(layer_per_t, p) * T) +
-                  static_cast<int64_t>(t[r]) * pick<NP>(tok_stride, p) + off0;
+    uint8_t *paged = reinterpret_cast<uint8_t *>(pbase) + paged_off + blk * blk_stride + in_blk * row_pitch + off0;
+    uint8_t *lm = lmc + lmc_fixed + lmc_per_t * T + static_cast<int64_t>(l) * (layer_fixed + layer_per_t * T) +
+                  static_cast<int64_t>(t[r]) * tok_stride + off0;
     src[r] = page2lmc ? paged : lm;
     dst[r] = page2lmc ? lm : paged;
     live[r] = t[r] < T && static_cast<uint64_t>(slot[r]) < static_cast<uint64_t>(job.num_slots);
