@@ -444,9 +444,24 @@ def bench_mla_576(torch, ops, dev, stream):
     store(); retr()
     t_s = time_events(torch, stream, store, 10)[0]
     t_r = time_events(torch, stream, retr, 10)[0]
+    # Ceilings for the same bytes: identity slots (blocks 0..255 in order, so
+    # every (layer, object) pair is one contiguous run on both sides) and the
+    # runtime's device copy of the whole payload at once.
+    ident = torch.arange(NR * TR, dtype=torch.int64, device=dev)
+    store_i = lambda: ops.multi_layer_kv_transfer_batched(objs, ptrs, ident, starts, dev, pbs4, True, True, 1, 0, 0, 0)
+    retr_i = lambda: ops.multi_layer_kv_transfer_batched(objs, ptrs, ident, starts, dev, pbs4, False, True, 1, 0, 0, 0)
+    store_i(); retr_i()
+    t_si = time_events(torch, stream, store_i, 10)[0]
+    t_ri = time_events(torch, stream, retr_i, 10)[0]
     P4 = L4 * NR * TR * W4 * ES
+    m_src = torch.empty(P4, dtype=torch.uint8, device=dev)
+    m_dst = torch.empty_like(m_src)
+    m_dst.copy_(m_src)
+    t_m = time_events(torch, stream, lambda: m_dst.copy_(m_src), 10)[0]
+    del m_src, m_dst
     out = {}
-    for name, t in (("mla576_store", t_s), ("mla576_retrieve", t_r)):
+    for name, t in (("mla576_store", t_s), ("mla576_retrieve", t_r), ("mla576_identity_slots_store", t_si),
+                    ("mla576_identity_slots_retrieve", t_ri), ("hipmemcpy_d2d_mla576_same_bytes", t_m)):
         out[name] = {"ms": round(t, 4), "payload_GBps": round(P4 / t / 1e6, 1),
                      "hbm_frac": round(2 * P4 / t / 1e6 / HBM_PEAK_GBS, 4)}
     del caches, objs
@@ -821,7 +836,28 @@ def main(argv=None):
         flash_retrieve()
         extra["d2d_flash_per_layer_calls_store"] = time_events(torch, stream, flash_store, 10)[0]
         extra["d2d_flash_per_layer_calls_retrieve"] = time_events(torch, stream, flash_retrieve, 10)[0]
-        del kvbuf
+        # Floors for one launch per layer: the same 32 calls with the identity
+        # slots (contiguous rows), and the runtime's device copy of the same
+        # 16 MiB per call.
+        lin_f = torch.arange(n_tok, dtype=torch.int64, device=dev)
+
+        def flash_identity():
+            for l in range(L):
+                ops.load_and_reshape_flash(kvbuf, flat[2 * l], flat[2 * l + 1], lin_f, l)
+
+        flash_identity()
+        extra["d2d_flash_per_layer_identity_slots_store"] = time_events(torch, stream, flash_identity, 10)[0]
+        lb = 2 * n_tok * W * ES
+        f_src = torch.empty(L * lb, dtype=torch.uint8, device=dev)
+        f_dst = torch.empty_like(f_src)
+
+        def memcpy_per_layer():
+            for l in range(L):
+                f_dst[l * lb:(l + 1) * lb].copy_(f_src[l * lb:(l + 1) * lb])
+
+        memcpy_per_layer()
+        extra["hipmemcpy_d2d_per_layer_16MiB"] = time_events(torch, stream, memcpy_per_layer, 10)[0]
+        del kvbuf, f_src, f_dst
 
     if "call_overhead" in sel:
         # Host time per drop-in call on a 1-token transfer, through the C++

@@ -235,8 +235,9 @@ __global__ void __launch_bounds__(kThreads)
 // Lean row kernel, for the common geometry: every plane's row is the same
 // power-of-two number of 2 KiB slices, the block size (when rows are block
 // strided) is a power of two, and plane p's pointer-table entry of layer l is
-// l * ppl + p * idx_step.  A wave owns one slice of one (plane, layer,
-// token); the grid is (slice groups, plane x layer, chunk).  Everything the
+// l * ppl + p * idx_step.  A wave owns kR consecutive slices of one (plane,
+// layer) (consecutive slices of a row, or the slices of consecutive tokens);
+// the grid is (slice groups, plane x layer, chunk).  Everything the
 // wave reads from its kernel arguments is at a fixed offset (all planes'
 // descriptors are read and one is selected), so one wait covers them; the
 // slot and the pointer-table entry are then loaded together, and the row
@@ -245,14 +246,25 @@ __global__ void __launch_bounds__(kThreads)
 // 256-token chunk (the connector's per-object call) pays on its first and
 // last waves.  Chunks of a launch hold at least one token (the host drops
 // empty ones).
+// Slices per wave: one for pointer-table launches (per-object calls), two
+// for flat per-layer launches (flash calls), whose 8192-row grids lose less
+// to dispatch with half the workgroups.  Measured on MI355X, 8B shape, three
+// interleaved runs: 16 per-object calls 0.215 ms with one slice per wave,
+// 0.224 with two, 0.232 with four; 32 flash calls (store / retrieve) 0.264 /
+// 0.255 ms with one, 0.259 / 0.243 with two, 0.281 / 0.267 with four.
 #ifndef LMC_KV_LEAN_R
-#define LMC_KV_LEAN_R 1           // lean kernel: slices per wave
+#define LMC_KV_LEAN_R 1
+#endif
+#ifndef LMC_KV_LEAN_R_FLAT
+#define LMC_KV_LEAN_R_FLAT 2
 #endif
 constexpr int kLeanR = LMC_KV_LEAN_R;
+constexpr int kLeanRFlat = LMC_KV_LEAN_R_FLAT;
 
 template <bool NT, int NC, bool TABLE, int NP, bool SLOT32>
 __global__ void __launch_bounds__(kThreads)
     kv_rows_lean(const CopyJob job, const ChunkListT<NC> chunks) {
+  constexpr int kR = TABLE ? kLeanR : kLeanRFlat;
   using V = u32x4;
   constexpr int kSlice = 64 * 16 * kSegs;
   const int c = NC == 1 ? 0 : static_cast<int>(blockIdx.z);
@@ -288,11 +300,11 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t tok_stride = pick(d0.lmc_token_stride, d1.lmc_token_stride, d2.lmc_token_stride);
   const int l = y - p * L;
   // Independent loads: the slots and the plane's paged base.
-  int t[kLeanR];
-  int64_t slot[kLeanR];
+  int t[kR];
+  int64_t slot[kR];
 #pragma unroll
-  for (int r = 0; r < kLeanR; ++r) {
-    t[r] = (item * kLeanR + r) >> spr_shift;
+  for (int r = 0; r < kR; ++r) {
+    t[r] = (item * kR + r) >> spr_shift;
     const int tc = t[r] < T ? t[r] : T - 1;  // in-range token for the slot load
     slot[r] = SLOT32 ? static_cast<int64_t>(static_cast<const int32_t *>(job.slots)[tok_start + tc])
                      : static_cast<const int64_t *>(job.slots)[tok_start + tc];
@@ -304,19 +316,19 @@ __global__ void __launch_bounds__(kThreads)
   // One wait covers all of these loads: without this the compiler places the
   // range check between them and issues the table load only after the slot.
 #pragma unroll
-  for (int r = 0; r < kLeanR; ++r) asm volatile("" ::"s"(slot[r]));
+  for (int r = 0; r < kR; ++r) asm volatile("" ::"s"(slot[r]));
   asm volatile("" ::"s"(pbase));
   // Addresses.  Flat rows are block rows with a zero shift (the host sets
   // blk_stride = row_pitch for them), so no branch splits the chain.
-  const uint8_t *src[kLeanR];
-  uint8_t *dst[kLeanR];
-  bool live[kLeanR];
+  const uint8_t *src[kR];
+  uint8_t *dst[kR];
+  bool live[kR];
   uintptr_t align = 0;
 #pragma unroll
-  for (int r = 0; r < kLeanR; ++r) {
+  for (int r = 0; r < kR; ++r) {
     const int64_t blk = slot[r] >> bs_shift;
     const int64_t in_blk = slot[r] & ((int64_t(1) << bs_shift) - 1);
-    const int64_t off0 = static_cast<int64_t>((item * kLeanR + r) & ((1 << spr_shift) - 1)) * kSlice;
+    const int64_t off0 = static_cast<int64_t>((item * kR + r) & ((1 << spr_shift) - 1)) * kSlice;
     uint8_t *paged = reinterpret_cast<uint8_t *>(pbase) + paged_off + blk * blk_stride + in_blk * row_pitch + off0;
     uint8_t *lm = lmc + lmc_fixed + lmc_per_t * T + static_cast<int64_t>(l) * (layer_fixed + layer_per_t * T) +
                   static_cast<int64_t>(t[r]) * tok_stride + off0;
@@ -329,20 +341,20 @@ __global__ void __launch_bounds__(kThreads)
   // slices to the byte path.
   if ((align & 15) != 0) {
 #pragma unroll
-    for (int r = 0; r < kLeanR; ++r)
+    for (int r = 0; r < kR; ++r)
       if (live[r])
         for (int o = lane; o < kSlice; o += 64) dst[r][o] = src[r][o];
     return;
   }
-  V v[kLeanR][kSegs];
+  V v[kR][kSegs];
 #pragma unroll
-  for (int r = 0; r < kLeanR; ++r)
+  for (int r = 0; r < kR; ++r)
     if (live[r])
 #pragma unroll
       for (int s = 0; s < kSegs; ++s)
         v[r][s] = ld<V, NT>(reinterpret_cast<const V *>(src[r] + (s * 64 + lane) * 16));
 #pragma unroll
-  for (int r = 0; r < kLeanR; ++r)
+  for (int r = 0; r < kR; ++r)
     if (live[r])
 #pragma unroll
       for (int s = 0; s < kSegs; ++s)
@@ -583,7 +595,7 @@ void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
     const int64_t max_tokens = max_rows / (job.n_planes * job.n_layers);
     const int64_t items = max_tokens * job.slices_per_row;
     check(items < (int64_t(1) << 31), "too many work items in one chunk");
-    const int64_t per_block = kWaves * kLeanR;
+    const int64_t per_block = kWaves * (job.table != nullptr ? kLeanR : kLeanRFlat);
     dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, (items + per_block - 1) / per_block)),
               job.n_layers * job.n_planes, n_chunks);
     launch_lean(job, chunks, n_chunks, grid, nt, stream);
