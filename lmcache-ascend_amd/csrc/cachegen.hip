@@ -1153,20 +1153,39 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
   uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
   const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
   if (!__any(tb.escapes)) {
+    // Four tokens per step: four lookups and one refill (a step starts with
+    // at least 33 valid bits and takes at most 32), the four table entries
+    // through the LDS transpose, and the transposed word of the previous
+    // step stored with its symbols extracted (entry >> 3 in every byte), so
+    // no step waits for its own transpose read.  The scheduling barrier
+    // keeps the store after the lookups: the compiler would otherwise hoist
+    // it, and its wait for the transpose read, above the first lookup.
+    // Measured on MI355X (symbol loop, shader cycles per symbol): a refill
+    // every two symbols and symbols extracted per step 158.6; the store one
+    // step late 150.4; one refill per four symbols 132.8; entries
+    // transposed 128.4.
     int t = 0;
+    uint32_t word = 0;
     for (; t + 4 <= T; t += 4) {
-      const uint32_t s0 = tb.step8(cur), s1 = tb.step8(cur);
+      const uint32_t e0 = tb.step8e(cur), e1 = tb.step8e(cur);
+      const uint32_t e2 = tb.step8e(cur), e3 = tb.step8e(cur);
       cur.refill();
-      const uint32_t s2 = tb.step8(cur), s3 = tb.step8(cur);
-      cur.refill();
-      obuf[lane] = static_cast<uint8_t>(s0);
-      obuf[kDecLanes + lane] = static_cast<uint8_t>(s1);
-      obuf[2 * kDecLanes + lane] = static_cast<uint8_t>(s2);
-      obuf[3 * kDecLanes + lane] = static_cast<uint8_t>(s3);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t > 0) {
+        *odst = (word >> 3) & 0x1F1F1F1Fu;
+        odst += step4;
+      }
+      obuf[lane] = static_cast<uint8_t>(e0);
+      obuf[kDecLanes + lane] = static_cast<uint8_t>(e1);
+      obuf[2 * kDecLanes + lane] = static_cast<uint8_t>(e2);
+      obuf[3 * kDecLanes + lane] = static_cast<uint8_t>(e3);
       wave_sync();
-      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      word = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      wave_sync();
+    }
+    if (t > 0) {
+      *odst = (word >> 3) & 0x1F1F1F1Fu;
       odst += step4;
-      wave_sync();
     }
     if (t < T) {
       for (int i = 0; t + i < T; ++i) {

@@ -13,10 +13,6 @@
 namespace lmc {
 namespace cgdec {
 
-#ifndef LMC_DEC_STEP_DWORD
-#define LMC_DEC_STEP_DWORD 1
-#endif
-
 constexpr int kPrec = 16;
 
 #ifdef __HIP__
@@ -158,8 +154,8 @@ struct LaneRegion {
 // Bit cursor over a lane region: a 64-bit window whose top `have` bits are
 // the stream's next bits (zeros past the end are real zeros), and `next`,
 // the region dword to append, read ahead.  refill() appends it when 32 bits
-// or fewer are left, so after a refill more than 32 bits are valid: two
-// codes of at most 8 bits, or one of at most 16, can be taken between
+// or fewer are left, so after a refill more than 32 bits are valid: four
+// codes of at most 8 bits, or two of at most 16, can be taken between
 // refills.
 struct LaneCursor {
   const uint32_t *w;
@@ -334,16 +330,12 @@ struct ByteTables {
   }
 
   // One symbol at a lane cursor for a table without escapes; returns the
-  // entry (symbol e >> 3, length (e & 7) + 1).  At most 8 bits are taken.
-  // One symbol at a lane cursor for a table without escapes; returns the
-  // symbol.  At most 8 bits are taken.  With LMC_DEC_STEP_DWORD the entry is
-  // taken from the dword holding entries 4 (e / 4) .. + 3, whose address
-  // needs only the window's top 6 bits, so the chain from one symbol to the
-  // next is shorter (two operations before the LDS read, a bit-field
-  // extract after it); otherwise the entry byte is read directly.
+  // symbol.  At most 8 bits are taken.  The entry is taken from the dword
+  // holding entries 4 (e / 4) .. + 3, whose address needs only the window's
+  // top 6 bits, so the chain from one symbol to the next is two operations
+  // before the LDS read and a bit-field extract and a shift after it.
   __device__ __forceinline__ uint32_t step8(LaneCursor &cur) const {
     const uint32_t hi = static_cast<uint32_t>(cur.win >> 32);
-#if LMC_DEC_STEP_DWORD
     // dword (e / 4) of the lane's column: table byte offset (e / 4) * 256 +
     // lane * 4, with e / 4 the window's top 6 bits; the table's LDS address
     // is a multiple of its 16 KiB size, so the offset is ORed in.
@@ -356,12 +348,21 @@ struct ByteTables {
     cur.win <<= (d >> sh) & 7u;
     cur.have -= static_cast<int>((d >> sh) & 7u) + 1;
     return (d >> (sh | 3u)) & 31u;
-#else
-    const uint32_t e = hi >> 24;
-    const uint32_t x = tab[((e << 6) | e) & 0x3F03u];
-    cur.consume(static_cast<int>(x & 7u) + 1);
-    return x >> 3;
-#endif
+  }
+
+  // step8 for the transposing loop: returns the table entry in the low
+  // byte (symbol << 3 | length - 1; the higher bytes hold other entries),
+  // whose symbols the caller extracts four at a time, one word per four
+  // tokens, instead of one symbol per step.
+  __device__ __forceinline__ uint32_t step8e(LaneCursor &cur) const {
+    const uint32_t hi = static_cast<uint32_t>(cur.win >> 32);
+    const uint32_t d = lds_dword(((hi >> 18) & 0x3F00u) | lane_at);
+    const uint32_t sh = (hi >> 21) & 0x18u;
+    const uint32_t l = (d >> sh) & 7u;
+    cur.win <<= 1;
+    cur.win <<= l;
+    cur.have -= static_cast<int>(l) + 1;
+    return d >> sh;
   }
 
   // Symbol and code length for the 16-bit window v.

@@ -171,6 +171,25 @@ int main(int argc, char **argv) {
                    nb, kind, tb.escapes ? 1 : 0, k, u, got[u], want[u]);
             return 1;
           }
+        // The kernel's four-token steps: four entries, one refill, symbols
+        // taken from the entries (entry >> 3); single steps for the tail.
+        if (!tb.escapes) {
+          lc.start(region.data(), n_dw);
+          for (t = 0; t + 4 <= T; t += 4) {
+            for (int j = 0; j < 4; ++j) got[t + j] = static_cast<uint8_t>((tb.step8e(lc) >> 3) & 31u);
+            lc.refill();
+          }
+          for (int i = 0; t < T; ++t, ++i) {
+            got[t] = static_cast<uint8_t>(tb.step8(lc));
+            if (i & 1) lc.refill();
+          }
+          for (int u = 0; u < T; ++u)
+            if (got[u] != want[u]) {
+              printf("STEP4 MISMATCH row %d (nb %d, kind %d) stream %d token %d: got %d want %d\n", it, nb, kind, k,
+                     u, got[u], want[u]);
+              return 1;
+            }
+        }
       }
       symbols += T;
     }
