@@ -1062,9 +1062,10 @@ __device__ __forceinline__ void decode_one_wave(uint8_t *lds, const int16_t *__r
 
 // Byte tables with per-lane stream regions (cgdec::LaneRegion): each lane
 // stages the 16-byte aligned chunks holding its own stream into its own LDS
-// region and rewrites them as big-endian dwords ending in a zero dword, so
-// the cursor (cgdec::LaneCursor, a 64-bit window refilled once per two codes
-// of at most 8 bits) reads region dwords without masking the stream's end.
+// region and zeroes what lies past the stream's end, so the cursor
+// (cgdec::LaneCursor, a 64-bit window refilled once per four codes of at
+// most 8 bits, each refill one byte permutation of two raw dwords) reads
+// the region without masking the stream's end.
 // Serves full 64-stream blocks with dword-aligned output rows whose regions
 // fit the LDS left after the tables and rows; returns false, having written
 // nothing, for any other block, which then takes decode_one_wave.
@@ -1144,9 +1145,9 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
       if (k0 + u < n_ch) reinterpret_cast<chunk16 *>(region)[k0 + u] = cv[u];
   }
   uint32_t *reg32 = reinterpret_cast<uint32_t *>(region);
-  const uint32_t n_dw = cgdec::LaneRegion::build(reg32, static_cast<uint32_t>(s_lo - a0), len);
+  cgdec::LaneRegion::seal(reg32, static_cast<uint32_t>(s_lo - a0), len);
   cgdec::LaneCursor cur;
-  cur.start(reg32, n_dw);
+  cur.start(reg32, static_cast<uint32_t>(s_lo - a0), len);
   uint8_t *obuf = lds + Tab::kBytes;
   uint8_t *out_blk = out + static_cast<int64_t>(bk.l) * T * C + bk.c0;
   // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.

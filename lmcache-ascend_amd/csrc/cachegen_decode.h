@@ -20,7 +20,17 @@ constexpr int kPrec = 16;
 __device__ __forceinline__ uint32_t lds_dword(uint32_t at) {
   return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(static_cast<uintptr_t>(at));
 }
+// Byte k of the result is byte sel.byte[k] (0..7) of the 64-bit hi:lo.
+__device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
 #else
+inline uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
+  uint32_t r = 0;
+  for (int k = 0; k < 4; ++k) r |= static_cast<uint32_t>((v >> (8 * ((sel >> (8 * k)) & 7u))) & 0xFFu) << (8 * k);
+  return r;
+}
 // Host build of this header (tests/decode_tables_check.cpp): the table lives
 // in host memory registered by host_lds_base.
 inline const uint8_t *&host_lds_base() {
@@ -122,56 +132,57 @@ struct BitCursor {
 // Per-lane stream regions.  A lane's stream, bytes [start, end) of the
 // concatenated stream buffer, is staged as the raw little-endian dwords of
 // the 16-byte aligned chunks that hold it (the first chunk starts at
-// start & ~15, so the stream begins `off` = start & 15 bytes in), and then
-// rewritten in place by LaneRegion::build as big-endian dwords of the stream
-// from its first byte, the bytes past its end zeroed, followed by one zero
-// dword.  A cursor over the region reads dword min(q, n_dw), so bits past
-// the stream's end read as zero without a mask on every read.
+// start & ~15, so the stream begins `off` = start & 15 bytes in), with 16
+// bytes of room after them.  LaneRegion::seal zeroes what a cursor reads
+// past the stream's end (the rest of the dword holding the end and the two
+// dwords after it), so bits past the end read as zero; the cursor forms
+// the stream's big-endian dword q from raw dwords off / 4 + q and the one
+// after it with one byte permutation (swap and alignment together).
+// An empty stream takes offset 0 (its region is the 16 bytes of room, which
+// hold the dwords read at offsets 0..3 only).
 struct LaneRegion {
-  // In place: region[0 .. n_dw) become the stream's big-endian dwords and
-  // region[n_dw] = 0; returns n_dw = ceil(len / 4).  The raw chunks must
-  // span at least off + len bytes plus one dword, so the read one dword
-  // ahead of the last output stays inside the region; output j reads raw
-  // dwords j + off / 4 and the one after it, never an earlier index than it
-  // writes, so the rewrite is safe in place.
-  static __device__ __forceinline__ uint32_t build(uint32_t *region, uint32_t off, uint32_t len) {
-    const uint32_t ph = off >> 2, r = off & 3u, n_dw = (len + 3u) >> 2;
-    uint32_t cur = region[ph];
-    for (uint32_t j = 0; j < n_dw; ++j) {
-      const uint32_t nxt = region[j + ph + 1u];
-      const uint64_t pair = (static_cast<uint64_t>(nxt) << 32) | cur;
-      uint32_t w = __builtin_bswap32(static_cast<uint32_t>(pair >> (8u * r)));
-      const uint32_t keep = len - 4u * j;  // bytes of this dword inside the stream, >= 1
-      w &= keep >= 4u ? 0xFFFFFFFFu : ~(0xFFFFFFFFu >> (8u * keep));
-      region[j] = w;
-      cur = nxt;
-    }
-    region[n_dw] = 0u;
-    return n_dw;
+  static __device__ __forceinline__ void seal(uint32_t *region, uint32_t off, uint32_t len) {
+    off = len ? off : 0u;
+    const uint32_t e = off + len, i = e >> 2, keep = e & 3u;
+    region[i] &= keep ? 0xFFFFFFFFu >> (32u - 8u * keep) : 0u;
+    region[i + 1] = 0u;
+    region[i + 2] = 0u;
   }
 };
 
-// Bit cursor over a lane region: a 64-bit window whose top `have` bits are
-// the stream's next bits (zeros past the end are real zeros), and `next`,
-// the region dword to append, read ahead.  refill() appends it when 32 bits
-// or fewer are left, so after a refill more than 32 bits are valid: four
-// codes of at most 8 bits, or two of at most 16, can be taken between
-// refills.
+// Bit cursor over a sealed lane region: a 64-bit window whose top `have`
+// bits are the stream's next bits (zeros past the end are real zeros), and
+// `next`, the stream dword to append, read ahead.  refill() appends it when
+// 32 bits or fewer are left, so after a refill more than 32 bits are valid:
+// four codes of at most 8 bits, or two of at most 16, can be taken between
+// refills.  Stream dword k reads raw dwords min(k, n_dw) + off / 4 and the
+// one after; from n_dw = ceil(len / 4) on that is sealed zeros.
 struct LaneCursor {
-  const uint32_t *w;
-  uint32_t zl;    // index of the region's zero dword (= n_dw)
-  uint32_t q;     // index of the dword in `next`
+  const uint32_t *w;  // raw region + off / 4
+  uint32_t sel;       // byte permutation for the stream's offset in its dword
+  uint32_t zl;        // n_dw
+  uint32_t q;         // index of the stream dword in next_lo / next_hi
   uint64_t win;
   int have;
-  uint32_t next;
+  uint32_t next_lo, next_hi;  // the raw dwords of stream dword q, read ahead
 
-  __device__ __forceinline__ void start(const uint32_t *region, uint32_t n_dw) {
-    w = region;
-    zl = n_dw;
-    win = (static_cast<uint64_t>(w[0]) << 32) | w[1u < zl ? 1u : zl];
+  // Big-endian: the result's top byte is the stream's first.
+  __device__ __forceinline__ uint32_t form(uint32_t hi, uint32_t lo) const { return byte_perm(hi, lo, sel); }
+  __device__ __forceinline__ void fetch(uint32_t k) {
+    const uint32_t c = k < zl ? k : zl;
+    next_lo = w[c];
+    next_hi = w[c + 1u];
+  }
+  __device__ __forceinline__ void start(const uint32_t *region, uint32_t off, uint32_t len) {
+    off = len ? off : 0u;
+    w = region + (off >> 2);
+    sel = 0x00010203u + (off & 3u) * 0x01010101u;
+    zl = (len + 3u) >> 2;
+    const uint32_t c1 = 1u < zl ? 1u : zl;
+    win = (static_cast<uint64_t>(form(w[1], w[0])) << 32) | form(w[c1 + 1u], w[c1]);
     have = 64;
     q = 2u;
-    next = w[q < zl ? q : zl];
+    fetch(q);
   }
   __device__ __forceinline__ uint32_t top8() const { return static_cast<uint32_t>(win >> 56); }
   __device__ __forceinline__ uint32_t top16() const { return static_cast<uint32_t>(win >> 48); }
@@ -179,13 +190,15 @@ struct LaneCursor {
     win <<= n;
     have -= n;
   }
+  // The raw dwords are permuted here, a refill after they were read, so
+  // their read is not waited for where it is issued.
   __device__ __forceinline__ void refill() {
     const bool need = have <= 32;
-    const uint64_t add = static_cast<uint64_t>(next) << ((32 - have) & 63);
+    const uint64_t add = static_cast<uint64_t>(form(next_hi, next_lo)) << ((32 - have) & 63);
     win |= need ? add : 0ull;
     have += need ? 32 : 0;
     q += need ? 1u : 0u;
-    next = w[q < zl ? q : zl];
+    fetch(q);
   }
 };
 

@@ -133,8 +133,8 @@ int main(int argc, char **argv) {
         }
       // The lane-region path: the stream's 16-byte aligned chunks of the
       // byte buffer (foreign bytes around it) as raw little-endian dwords,
-      // plus 4 garbage dwords, rewritten in place, then decoded with the
-      // lane cursor: two codes per refill without escapes, one with.
+      // plus 4 garbage dwords, sealed past the stream's end, then decoded
+      // with the lane cursor: two codes per refill without escapes, one with.
       {
         const uint32_t a0 = lo & ~15u;
         const uint32_t n_ch = len ? ((hi - 1) / 16 - lo / 16 + 1) : 0;
@@ -142,9 +142,9 @@ int main(int argc, char **argv) {
         for (auto &x : region) x = static_cast<uint32_t>(rng());
         for (uint32_t i = 0; i < 16 * n_ch; ++i)
           reinterpret_cast<uint8_t *>(region.data())[i] = win_bytes[a0 + i];
-        const uint32_t n_dw = lmc::cgdec::LaneRegion::build(region.data(), lo - a0, len);
+        lmc::cgdec::LaneRegion::seal(region.data(), lo - a0, len);
         lmc::cgdec::LaneCursor lc;
-        lc.start(region.data(), n_dw);
+        lc.start(region.data(), lo - a0, len);
         int t = 0;
         if (!tb.escapes) {
           for (; t + 2 <= T; t += 2) {
@@ -174,7 +174,7 @@ int main(int argc, char **argv) {
         // The kernel's four-token steps: four entries, one refill, symbols
         // taken from the entries (entry >> 3); single steps for the tail.
         if (!tb.escapes) {
-          lc.start(region.data(), n_dw);
+          lc.start(region.data(), lo - a0, len);
           for (t = 0; t + 4 <= T; t += 4) {
             for (int j = 0; j < 4; ++j) got[t + j] = static_cast<uint8_t>((tb.step8e(lc) >> 3) & 31u);
             lc.refill();

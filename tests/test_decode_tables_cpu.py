@@ -23,8 +23,10 @@ def checker(tmp_path_factory):
     obj = d / "oracle_cachegen.o"
     exe = d / "decode_tables_check"
     subprocess.run(["gcc", "-O2", "-c", os.path.join(REPO, "oracle", "cachegen.c"), "-o", str(obj)], check=True)
-    subprocess.run(["g++", "-O2", "-std=c++17", os.path.join(HERE, "decode_tables_check.cpp"), str(obj),
-                    "-o", str(exe)], check=True)
+    # Built with AddressSanitizer: the lane regions are sized exactly as in
+    # the kernel, so a read or write past a lane's region fails the run.
+    subprocess.run(["g++", "-O1", "-std=c++17", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                    os.path.join(HERE, "decode_tables_check.cpp"), str(obj), "-o", str(exe)], check=True)
     return str(exe)
 
 
