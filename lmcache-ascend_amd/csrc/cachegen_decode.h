@@ -299,26 +299,44 @@ struct ByteTables {
   }
 
   // Running maximum over dwords [d0, d1) starting from `carry` (the entry
-  // before dword d0, 0 for d0 = 0).
+  // before dword d0, 0 for d0 = 0).  One dword takes four byte maxima, each
+  // written into its byte of the dword in place (SDWA with the other bytes
+  // preserved), byte 0 against the previous dword's byte 3.
+  __device__ __forceinline__ static uint32_t scan_dword(uint32_t w, uint32_t prev) {
+#ifdef __HIP_DEVICE_COMPILE__
+    asm("v_max_u32_sdwa %0, %1, %0 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3 src1_sel:BYTE_0"
+        : "+v"(w) : "v"(prev));
+    asm("v_max_u32_sdwa %0, %0, %0 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0 src1_sel:BYTE_1"
+        : "+v"(w));
+    asm("v_max_u32_sdwa %0, %0, %0 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_2"
+        : "+v"(w));
+    asm("v_max_u32_sdwa %0, %0, %0 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2 src1_sel:BYTE_3"
+        : "+v"(w));
+    return w;
+#else
+    uint32_t carry = prev >> 24, o = 0;
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = (w >> (8 * i)) & 0xFFu;
+      carry = carry > v ? carry : v;
+      o |= carry << (8 * i);
+    }
+    return o;
+#endif
+  }
   __device__ __forceinline__ void scan(int d0, int d1, uint32_t carry) {
     uint32_t *t32 = reinterpret_cast<uint32_t *>(tab);
+    uint32_t prev = carry << 24;
     for (int d = d0; d < d1; d += 8) {
       uint32_t w[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) w[k] = t32[(d + k) * kLanes];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        uint32_t o = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t v = (w[k] >> (8 * i)) & 0xFFu;
-          carry = carry > v ? carry : v;
-          o |= carry << (8 * i);
-        }
-        t32[(d + k) * kLanes] = o;
+        prev = scan_dword(w[k], prev);
+        t32[(d + k) * kLanes] = prev;
       }
     }
-    escapes = carry == kEscape;
+    escapes = (prev >> 24) == kEscape;
   }
 
   // top, which only the binary search reads.
