@@ -24,7 +24,10 @@ __device__ __forceinline__ uint32_t lds_dword(uint32_t at) {
 __device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
+// True in every lane when b holds in some lane of the wave.
+__device__ __forceinline__ bool wave_any(bool b) { return __any(b); }
 #else
+inline bool wave_any(bool b) { return b; }
 inline uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
   uint32_t r = 0;
@@ -262,7 +265,10 @@ struct ByteTables {
   // the first symbol whose base is below an earlier one, or nb; every
   // symbol from the wrap on has base 0x10000 and writes nothing.  Writes
   // that fall outside the table go to `dummy`, a byte of the caller's, so
-  // the loops have no branches.
+  // the loops have no branches.  When no row of the wave has a base off a
+  // multiple of 256 (calculate_cdf's rows; checked for nb == kMaxBins, where
+  // every loaded entry belongs to the row), no base writes an escape, and
+  // the loop without those writes is taken.
   __device__ __forceinline__ void mark(uint8_t *dummy) {
     uint32_t rw[kMaxBins];
 #pragma unroll
@@ -276,6 +282,21 @@ struct ByteTables {
       top_base = max(top_base, v);
     }
     row.wrap = wrap;
+    bool aligned = false;
+    if (nb == kMaxBins) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int s = 0; s < kMaxBins; ++s) acc |= rw[s];
+      aligned = !wave_any((acc & 0xF0u) != 0);
+    }
+    if (aligned)
+      mark_rows<true>(rw, wrap, dummy);
+    else
+      mark_rows<false>(rw, wrap, dummy);
+  }
+
+  template <bool kAligned>
+  __device__ __forceinline__ void mark_rows(const uint32_t (&rw)[kMaxBins], int wrap, uint8_t *dummy) {
     uint32_t base = rw[0] & 0xFFF0u;
 #pragma unroll
     for (int s = 0; s < kMaxBins; ++s) {
@@ -288,6 +309,9 @@ struct ByteTables {
       const uint32_t code = len - 1u < 8u ? ((static_cast<uint32_t>(s) << 3) | (len - 1u)) : kEscape;
       if (s == 0) {  // owns the windows below every later base: prefix 0
         *entry(0) = static_cast<uint8_t>(code);
+      } else if (kAligned) {
+        // base is a multiple of 256, or 0x10000 from the wrap on (no entry).
+        *(base < 0x10000u ? entry(base >> 8) : dummy) = static_cast<uint8_t>(code);
       } else {
         // base is 0x10000 from the wrap on: no escape (its low byte is 0)
         // and no entry (it is not below 0xFF01).
