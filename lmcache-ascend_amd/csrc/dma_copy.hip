@@ -28,6 +28,7 @@
 // caller's order on the copy engines, merging only consecutive adjacent
 // rows, which keeps the last-writer-wins result of the reference.
 #include "common.h"
+#include "gmem.h"
 
 #include <algorithm>
 #include <atomic>
@@ -81,13 +82,13 @@ __global__ void __launch_bounds__(kSegThreads) seg_copy(SegTable t) {
         V v[kSegUnroll];
 #pragma unroll
         for (int k = 0; k < kSegUnroll; ++k)
-          v[k] = reinterpret_cast<const V *>(src)[k * kSegThreads + threadIdx.x];
+          v[k] = gload(reinterpret_cast<const V *>(src) + k * kSegThreads + threadIdx.x);
 #pragma unroll
         for (int k = 0; k < kSegUnroll; ++k)
-          reinterpret_cast<V *>(dst)[k * kSegThreads + threadIdx.x] = v[k];
+          gstore(reinterpret_cast<V *>(dst) + k * kSegThreads + threadIdx.x, v[k]);
       } else {
         for (uint32_t k = threadIdx.x; k < nv; k += kSegThreads)
-          reinterpret_cast<V *>(dst)[k] = reinterpret_cast<const V *>(src)[k];
+          gstore(reinterpret_cast<V *>(dst) + k, gload(reinterpret_cast<const V *>(src) + k));
       }
       for (uint32_t b = nv * 16 + threadIdx.x; b < n; b += kSegThreads) dst[b] = src[b];
     } else {

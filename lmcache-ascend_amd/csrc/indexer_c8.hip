@@ -24,6 +24,7 @@
 // (bytewise when the packet is not 16-byte aligned) and one lane per token
 // its scale.  Every access is bounded by the checks above.
 #include "common.h"
+#include "gmem.h"
 
 #include <algorithm>
 #include <cstring>
@@ -120,7 +121,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
       const V *src = reinterpret_cast<const V *>(packet + tok(u) * kb);
 #pragma unroll
       for (int k = 0; k < kKeyVecs; ++k)
-        if (gl + k * kC8Group < nv) x[u][k] = src[gl + k * kC8Group];
+        if (gl + k * kC8Group < nv) x[u][k] = gload(src + gl + k * kC8Group);
     }
   }
   int64_t phys[kC8Unroll];
@@ -146,7 +147,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
         const V *src = reinterpret_cast<const V *>(L.keys + phys[u] * kb);
 #pragma unroll
         for (int k = 0; k < kKeyVecs; ++k)
-          if (gl + k * kC8Group < nv) x[u][k] = src[gl + k * kC8Group];
+          if (gl + k * kC8Group < nv) x[u][k] = gload(src + gl + k * kC8Group);
       }
     }
 #pragma unroll
@@ -155,7 +156,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
       V *dst = reinterpret_cast<V *>(job.from_npu ? packet + tok(u) * kb : L.keys + phys[u] * kb);
 #pragma unroll
       for (int k = 0; k < kKeyVecs; ++k)
-        if (gl + k * kC8Group < nv) dst[gl + k * kC8Group] = x[u][k];
+        if (gl + k * kC8Group < nv) gstore(dst + gl + k * kC8Group, x[u][k]);
     }
   } else {
 #pragma unroll

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "gmem.h"
 
 #include <algorithm>
 #include <cstring>
@@ -48,9 +49,12 @@ template <> struct VecOf<1> { using T = uint8_t; };
 #define LMC_KV_NT_STORES 1        // streaming hint on stores of HBM copies
 #endif
 
+// Loads and stores through the global address space (gmem.h).
 template <typename T, bool NT> __device__ __forceinline__ T ld(const T *p) {
-  if constexpr (NT && LMC_KV_NT_LOADS) return __builtin_nontemporal_load(p);
-  else return *p;
+  if constexpr (NT && LMC_KV_NT_LOADS)
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const __attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p)));
+  else return gload(p);
 }
 typedef __attribute__((address_space(1))) u32x4 GlobalU32x4;
 
@@ -68,8 +72,9 @@ template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
   if constexpr (NT && LMC_KV_WT_STORES && sizeof(T) == 16)
     __builtin_amdgcn_global_store_b128((GlobalU32x4 *)(p),
                                        __builtin_bit_cast(u32x4, v), "agent");
-  else if constexpr (NT && LMC_KV_NT_STORES) __builtin_nontemporal_store(v, p);
-  else *p = v;
+  else if constexpr (NT && LMC_KV_NT_STORES)
+    __builtin_nontemporal_store(v, reinterpret_cast<__attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p)));
+  else gstore(p, v);
 }
 
 inline int64_t gcd64(int64_t a, int64_t b) {

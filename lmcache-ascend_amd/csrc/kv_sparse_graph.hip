@@ -19,6 +19,7 @@
 // one entry and issues both rows' loads before their stores; rows whose
 // source or destination is not 16-byte aligned are copied bytewise.
 #include "common.h"
+#include "gmem.h"
 
 #include <algorithm>
 #include <cstring>
@@ -58,7 +59,7 @@ __device__ __forceinline__ void sfa_row(uint8_t *dst, const uint8_t *src,
                                         int bytes, int gl, int G) {
   if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
     for (int v = gl; v < bytes / 16; v += G)
-      reinterpret_cast<SfaVec *>(dst)[v] = reinterpret_cast<const SfaVec *>(src)[v];
+      gstore(reinterpret_cast<SfaVec *>(dst) + v, gload(reinterpret_cast<const SfaVec *>(src) + v));
   } else {
     for (int b = gl; b < bytes; b += G) dst[b] = src[b];
   }
@@ -104,14 +105,14 @@ __global__ void __launch_bounds__(kSfaThreads) sfa_copy(SfaJob job) {
 #pragma unroll
     for (int u = 0; u < kSfaUnroll; ++u) {
       const int v = gl + u * G;
-      if (v < kv) xk[u] = reinterpret_cast<const SfaVec *>(ksrc)[v];
-      if (v < pv) xp[u] = reinterpret_cast<const SfaVec *>(psrc)[v];
+      if (v < kv) xk[u] = gload(reinterpret_cast<const SfaVec *>(ksrc) + v);
+      if (v < pv) xp[u] = gload(reinterpret_cast<const SfaVec *>(psrc) + v);
     }
 #pragma unroll
     for (int u = 0; u < kSfaUnroll; ++u) {
       const int v = gl + u * G;
-      if (v < kv) reinterpret_cast<SfaVec *>(kdst)[v] = xk[u];
-      if (v < pv) reinterpret_cast<SfaVec *>(pdst)[v] = xp[u];
+      if (v < kv) gstore(reinterpret_cast<SfaVec *>(kdst) + v, xk[u]);
+      if (v < pv) gstore(reinterpret_cast<SfaVec *>(pdst) + v, xp[u]);
     }
     return;
   }
