@@ -277,9 +277,15 @@ def bench_rope(torch, ops, dev, stream):
     new = old + 1000
     t = time_events(torch, stream, lambda: ops.rotary_embedding_k_fused(old, new, k, Dh, cache, True), 20)[0]
     nbytes = 2 * k.numel() * 2 + 2 * T * Dh * 2 + 16 * T
+    # The floor for one launch moving this much: the runtime's device copy
+    # of the same 8 MiB of K (read once, written once).
+    k2 = torch.empty_like(k)
+    t_copy = time_events(torch, stream, lambda: k2.copy_(k), 20)[0]
     return {"rope_k_fused": {"ms": round(t, 4), "GBps": round(nbytes / t / 1e6, 1),
                              "hbm_frac": round(nbytes / t / 1e6 / HBM_PEAK_GBS, 4),
-                             "tokens_per_s": round(T / t * 1e3)}}
+                             "tokens_per_s": round(T / t * 1e3)},
+            "hipmemcpy_d2d_rope_key_8MiB": {"ms": round(t_copy, 4),
+                                            "GBps": round(2 * k.numel() * 2 / t_copy / 1e6, 1)}}
 
 
 def bench_blend(torch, ops, dev, stream, flat, slots):
