@@ -126,6 +126,25 @@ int lmc_fused_multi_layer_kv_transfer(
     int32_t use_mla, int32_t kvcache_format, int64_t k_hidden_dims,
     int64_t v_hidden_dims, int64_t dsa_hidden_dims, void *stream);
 
+/* No counterpart in the reference.  lmc_fused_multi_layer_kv_transfer for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc): the staging buffer is the library's
+ * own static device area of LMC_NOALLOC_STAGING_BYTES per GPU (resolved once
+ * per device on the first call), so the call allocates nothing; a transfer
+ * needing more staging than that is refused with LMC_ERR_RUNTIME.  The
+ * staging device is `paged_device` (the current device when negative).  A
+ * store zeroes the staging bytes first (a fill kernel), so rows of skipped
+ * slots arrive in `key_value` as zeros, as with a zeroed staging_cache.
+ * Every call on one GPU shares that GPU's area: calls that overlap on one GPU
+ * (on different streams, or from different threads) race. */
+#define LMC_NOALLOC_STAGING_BYTES (64ll << 20)
+int lmc_fused_multi_layer_kv_transfer_noalloc(
+    const lmc_tensor *key_value, const lmc_tensor *key_value_ptrs,
+    const lmc_tensor *slot_mapping, int32_t paged_device,
+    int64_t page_buffer_size, int32_t direction, int32_t use_mla,
+    int32_t kvcache_format, int64_t k_hidden_dims, int64_t v_hidden_dims,
+    int64_t dsa_hidden_dims, void *stream);
+
 /* Replaces single_layer_kv_transfer (csrc/mem_kernels.cpp:265-334; planner
  * csrc/utils.cpp:212-406; validation csrc/utils.cpp:903-966; pybind
  * csrc/pybind.cpp:467-472).  `caches` holds the n_caches paged tensors of

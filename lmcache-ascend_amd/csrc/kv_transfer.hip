@@ -32,6 +32,8 @@
 // 379-380); skipping is the superset.
 #include "kv_geom.h"
 
+#include <mutex>
+
 namespace lmc {
 
 // Launch geometry (compile-time; the defaults are the measured best on
@@ -1128,6 +1130,98 @@ int64_t fused_required_size(int fmt, bool use_mla, int64_t L, int64_t T,
   }
 }
 
+// Staging area of lmc_fused_multi_layer_kv_transfer_noalloc: one memory
+// object of up to LMC_NOALLOC_STAGING_BYTES, allocated per GPU when the
+// code object loads and held until the process ends.  Host code never uses
+// this name as an address: it is resolved once per device with
+// hipGetSymbolAddress (noalloc_staging below).
+static __device__ __align__(256) uint8_t scratch[LMC_NOALLOC_STAGING_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint8_t *g_noalloc_ptr[kMaxDevices] = {};
+
+// Device address of `device`'s staging area; resolved on the first call per
+// device, with that device current.
+uint8_t *noalloc_staging(int device) {
+  check(device >= 0 && device < kMaxDevices,
+        "fused_multi_layer_kv_transfer_noalloc: device " +
+            std::to_string(device) + " out of range");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_ptr[device] == nullptr) {
+    DeviceGuard guard(device);
+    void *p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+              "hipGetSymbolAddress(staging area)");
+    check(p != nullptr, "hipGetSymbolAddress returned a null staging area");
+    g_noalloc_ptr[device] = static_cast<uint8_t *>(p);
+  }
+  return g_noalloc_ptr[device];
+}
+
+// Zeroes `n16` 16-byte words from `p` (a fill kernel, not hipMemsetAsync, so
+// the call can be recorded into a HIP graph).
+__global__ void __launch_bounds__(256) zero_words(u32x4 *p, int64_t n16) {
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    gstore(p + i, z);
+}
+
+// fused_multi_layer_kv_transfer through a staging buffer of `capacity`
+// bytes at `stg_data` on device `stg_device` (csrc/mem_kernels.cpp:113-213):
+// H2D copy into the staging buffer before a load, the gather/scatter against
+// it, D2H copy out of it after a store.  `clear_before_store` zeroes the
+// staging bytes of a store first, so rows of skipped slots leave as zeros.
+void fused_transfer(const lmc_tensor &kv, uint8_t *stg_data, int stg_device,
+                    int64_t capacity, const char *too_small,
+                    bool clear_before_store, const lmc_tensor *key_value_ptrs,
+                    const lmc_tensor *slot_mapping, int32_t paged_device,
+                    int64_t page_buffer_size, bool direction, bool use_mla,
+                    int32_t kvcache_format, int64_t k_hidden_dims,
+                    int64_t v_hidden_dims, int64_t dsa_hidden_dims,
+                    hipStream_t s) {
+  const lmc_tensor &slots = slots_of(slot_mapping);
+  check(kv.ndim >= 2, "key_value must have at least 2 dims");
+  const int64_t L = size(kv, 1), W = size(kv, -1), es = elem_size(kv);
+  const int64_t T = slots.sizes[0];
+  const int64_t required = fused_required_size(
+      kvcache_format, use_mla, L, T, W, k_hidden_dims, v_hidden_dims,
+      dsa_hidden_dims, es);
+  check(capacity >= required, std::string(too_small) + ": need " +
+                                  std::to_string(required) + " bytes, got " +
+                                  std::to_string(capacity));
+  check(nbytes(kv) >= required, "key_value is smaller than the transfer");
+  DeviceGuard guard(paged_device >= 0 ? paged_device : stg_device);
+  if (!direction && required > 0)
+    hip_check(hipMemcpyAsync(stg_data, kv.data, required,
+                             hipMemcpyHostToDevice, s),
+              "H2D memcpy failed: cpu_buffer -> staging_cache");
+  if (direction && clear_before_store && required > 0) {
+    const int64_t n16 = (required + 15) / 16;  // capacity is a multiple of 16
+    const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_words, dim3(static_cast<uint32_t>(blocks)),
+                       dim3(256), 0, s, reinterpret_cast<u32x4 *>(stg_data),
+                       n16);
+    hip_check(hipGetLastError(), "zero_words launch");
+  }
+  // The staging buffer is used as a flat buffer with key_value's logical
+  // layout from its data pointer, whatever its view strides
+  // (csrc/mem_kernels.cpp:124-126, 183-207); its capacity was checked
+  // against `required` above.
+  lmc_tensor view = kv;
+  view.data = stg_data;
+  view.device = stg_device;
+  run_multi_layer(&view, 1, nullptr, key_value_ptrs, slot_mapping,
+                  paged_device, page_buffer_size, direction, use_mla,
+                  kvcache_format, k_hidden_dims, v_hidden_dims,
+                  dsa_hidden_dims, s, false);
+  if (direction && required > 0)
+    hip_check(hipMemcpyAsync(kv.data, stg_data, required,
+                             hipMemcpyDeviceToHost, s),
+              "D2H memcpy failed: staging_cache -> cpu_buffer");
+}
+
 } // namespace lmc
 
 using namespace lmc;
@@ -1176,40 +1270,34 @@ int lmc_fused_multi_layer_kv_transfer(
   return guarded([&] {
     const lmc_tensor &kv = deref(key_value, "key_value");
     const lmc_tensor &stg = deref(staging_cache, "staging_cache");
-    const lmc_tensor &slots = slots_of(slot_mapping);
-    check(kv.ndim >= 2, "key_value must have at least 2 dims");
     check(stg.device >= 0, "staging_cache must be a device tensor");
-    const int64_t L = size(kv, 1), W = size(kv, -1), es = elem_size(kv);
-    const int64_t T = slots.sizes[0];
-    const int64_t required = fused_required_size(
-        kvcache_format, use_mla != 0, L, T, W, k_hidden_dims, v_hidden_dims,
-        dsa_hidden_dims, es);
-    const int64_t staging_size = nbytes(stg);
-    check(staging_size >= required,
-          "staging_cache size insufficient: need " + std::to_string(required) +
-              " bytes, got " + std::to_string(staging_size));
-    check(nbytes(kv) >= required, "key_value is smaller than the transfer");
-    hipStream_t s = as_stream(stream);
-    DeviceGuard guard(paged_device >= 0 ? paged_device : stg.device);
-    if (!direction && required > 0)
-      hip_check(hipMemcpyAsync(stg.data, kv.data, required,
-                               hipMemcpyHostToDevice, s),
-                "H2D memcpy failed: cpu_buffer -> staging_cache");
-    // The staging buffer is used as a flat buffer with key_value's logical
-    // layout from its data pointer, whatever its view strides
-    // (csrc/mem_kernels.cpp:124-126, 183-207); its capacity was checked
-    // against `required` above.
-    lmc_tensor view = kv;
-    view.data = stg.data;
-    view.device = stg.device;
-    run_multi_layer(&view, 1, nullptr, key_value_ptrs, slot_mapping,
-                    paged_device, page_buffer_size, direction != 0,
-                    use_mla != 0, kvcache_format, k_hidden_dims,
-                    v_hidden_dims, dsa_hidden_dims, s, false);
-    if (direction && required > 0)
-      hip_check(hipMemcpyAsync(kv.data, stg.data, required,
-                               hipMemcpyDeviceToHost, s),
-                "D2H memcpy failed: staging_cache -> cpu_buffer");
+    fused_transfer(kv, static_cast<uint8_t *>(stg.data), stg.device,
+                   nbytes(stg), "staging_cache size insufficient", false,
+                   key_value_ptrs, slot_mapping, paged_device,
+                   page_buffer_size, direction != 0, use_mla != 0,
+                   kvcache_format, k_hidden_dims, v_hidden_dims,
+                   dsa_hidden_dims, as_stream(stream));
+  });
+}
+
+int lmc_fused_multi_layer_kv_transfer_noalloc(
+    const lmc_tensor *key_value, const lmc_tensor *key_value_ptrs,
+    const lmc_tensor *slot_mapping, int32_t paged_device,
+    int64_t page_buffer_size, int32_t direction, int32_t use_mla,
+    int32_t kvcache_format, int64_t k_hidden_dims, int64_t v_hidden_dims,
+    int64_t dsa_hidden_dims, void *stream) {
+  return guarded([&] {
+    const lmc_tensor &kv = deref(key_value, "key_value");
+    int device = paged_device;
+    if (device < 0) hip_check(hipGetDevice(&device), "hipGetDevice");
+    uint8_t *stg = noalloc_staging(device);
+    fused_transfer(kv, stg, device, LMC_NOALLOC_STAGING_BYTES,
+                   "fused_multi_layer_kv_transfer_noalloc: the transfer "
+                   "exceeds the library's staging area",
+                   true, key_value_ptrs, slot_mapping, device,
+                   page_buffer_size, direction != 0, use_mla != 0,
+                   kvcache_format, k_hidden_dims, v_hidden_dims,
+                   dsa_hidden_dims, as_stream(stream));
   });
 }
 

@@ -235,6 +235,41 @@ def fused_multi_layer_kv_transfer(
     )
 
 
+# Bytes of the library's per-GPU staging area used by
+# fused_multi_layer_kv_transfer_noalloc.
+NOALLOC_STAGING_BYTES = 64 << 20
+
+
+def fused_multi_layer_kv_transfer_noalloc(
+    key_value: torch.Tensor,
+    key_value_ptrs: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    paged_memory_device: torch.device,
+    page_buffer_size: int,
+    direction: bool,
+    use_mla: bool,
+    kvcache_format_raw: int,
+    k_hidden_dims: int = 0,
+    v_hidden_dims: int = 0,
+    dsa_hidden_dims: int = 0,
+) -> None:
+    """fused_multi_layer_kv_transfer without a staging_cache argument, for
+    callers that cannot allocate device memory: the library stages through
+    its own NOALLOC_STAGING_BYTES area on the cache device and allocates
+    nothing.  A store zeroes the staging bytes first, so rows of skipped
+    slots arrive as zeros.  Calls overlapping on one GPU share that area and
+    race."""
+    dev = _device_index(paged_memory_device, key_value_ptrs)
+    a, p, s = _desc(key_value), _desc(key_value_ptrs), _desc(slot_mapping)
+    _run(
+        _L.lmc_fused_multi_layer_kv_transfer_noalloc(
+            _ref(a), _ref(p), _ref(s), dev, int(page_buffer_size),
+            int(bool(direction)), int(bool(use_mla)), int(kvcache_format_raw),
+            int(k_hidden_dims), int(v_hidden_dims), int(dsa_hidden_dims), _stream(dev),
+        )
+    )
+
+
 def multi_layer_kv_transfer_unilateral(*args, **kwargs):
     """csrc/mem_kernels.cpp:255-263: not implemented in the reference either."""
     raise NotImplementedError("multi_layer_kv_transfer_unilateral is not implemented.")
