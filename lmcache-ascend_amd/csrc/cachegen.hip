@@ -411,6 +411,13 @@ __global__ void __launch_bounds__(kEncLanes)
 //      and only bytes below min(chunk, stream length), as the single-lane
 //      encoder writes them.
 constexpr int kEncWaves = 4;
+#ifndef LMC_ENC_SPLIT
+#define LMC_ENC_SPLIT 1     // split encoder for full 64-channel blocks
+#endif
+#ifndef LMC_ENC_PIECES
+#define LMC_ENC_PIECES 8    // waves (token pieces) per block of the split encoder
+#endif
+constexpr int kEncPieces = LMC_ENC_PIECES;
 constexpr int kEncTileThreads = kEncLanes * kEncWaves;
 constexpr int kEncTileMaxT = 4 * kEncLanes;
 
@@ -437,6 +444,59 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return static_cast<uint32_t>(x);
 }
 
+// Encode staging: the block's CDF rows (contiguous in memory) into `stage`
+// and its symbols, transposed to one row of `sym_stride` words per stream,
+// into `tile`; every global load of a thread is issued before its LDS
+// stores.  With `vec_tile` (a full block of 64 channels, C % 16 == 0 and a
+// 16-byte aligned input) each token's 64 symbols are four 16-byte loads.
+template <int NT>
+__device__ __forceinline__ void enc_stage(const int16_t *__restrict__ cdf,
+                                          const uint8_t *__restrict__ in, int T, int C, int nb,
+                                          int l, int c0, int cnt, int64_t s0, int vec_tile,
+                                          int sym_stride, int16_t *stage, uint8_t *tile) {
+  const int tid = static_cast<int>(threadIdx.x);
+  const int16_t *rsrc = cdf + s0 * (nb + 1);
+  const int rcount = cnt * (nb + 1);
+  constexpr int kR = 4;
+  int16_t rv[kR];
+  int ri[kR];
+#pragma unroll
+  for (int k = 0; k < kR; ++k) {
+    const int i = k * NT + tid;
+    ri[k] = i < rcount ? i : rcount - 1;
+    rv[k] = rsrc[ri[k]];
+  }
+  const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
+  const int pieces = T * 4;
+  const int row_bytes = sym_stride * 4;
+  if (vec_tile && cnt == kEncLanes) {
+    constexpr int kV = (4 * kEncTileMaxT + NT - 1) / NT;  // 16-byte pieces per thread (T <= 256)
+    uint4 v[kV];
+    int pi[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int i = k * NT + tid;
+      pi[k] = i < pieces ? i : pieces - 1;
+      v[k] = *reinterpret_cast<const uint4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16);
+    }
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      uint8_t *d = tile + (pi[k] & 3) * 16 * row_bytes + (pi[k] >> 2);
+      const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) d[j * row_bytes] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
+    }
+  } else {
+    for (int i = tid; i < T * kEncLanes; i += NT) {
+      const int c = i % kEncLanes, t = i / kEncLanes;
+      tile[c * row_bytes + t] = c < cnt ? src[static_cast<int64_t>(t) * C + c] : 0;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kR; ++k) stage[ri[k]] = rv[k];
+  for (int i = kR * NT + tid; i < rcount; i += NT) stage[i] = rsrc[i];
+}
+
 __global__ void __launch_bounds__(kEncTileThreads)
     encode_wave_kernel(const int16_t *__restrict__ cdf,
                        const uint8_t *__restrict__ in, int T, int C, int nb,
@@ -458,47 +518,7 @@ __global__ void __launch_bounds__(kEncTileThreads)
   uint32_t *bitbuf = lds + rows_words + kEncLanes * sym_stride + 2 * wv * cap_words;
 
   // 1. Rows and symbols: every load of the thread, then the LDS stores.
-  {
-    const int16_t *rsrc = cdf + s0 * (nb + 1);
-    const int rcount = cnt * (nb + 1);
-    constexpr int kR = 4;
-    int16_t rv[kR];
-    int ri[kR];
-#pragma unroll
-    for (int k = 0; k < kR; ++k) {
-      const int i = k * kEncTileThreads + tid;
-      ri[k] = i < rcount ? i : rcount - 1;
-      rv[k] = rsrc[ri[k]];
-    }
-    const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
-    const int pieces = T * 4;
-    const int row_bytes = sym_stride * 4;
-    if (vec_tile && cnt == kEncLanes) {
-      uint4 v[4];
-      int pi[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = k * kEncTileThreads + tid;
-        pi[k] = i < pieces ? i : pieces - 1;
-        v[k] = *reinterpret_cast<const uint4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        uint8_t *d = tile + (pi[k] & 3) * 16 * row_bytes + (pi[k] >> 2);
-        const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j) d[j * row_bytes] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
-      }
-    } else {
-      for (int i = tid; i < T * kEncLanes; i += kEncTileThreads) {
-        const int c = i % kEncLanes, t = i / kEncLanes;
-        tile[c * row_bytes + t] = c < cnt ? src[static_cast<int64_t>(t) * C + c] : 0;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kR; ++k) stage[ri[k]] = rv[k];
-    for (int i = kR * kEncTileThreads + tid; i < rcount; i += kEncTileThreads) stage[i] = rsrc[i];
-  }
+  enc_stage<kEncTileThreads>(cdf, in, T, C, nb, l, c0, cnt, s0, vec_tile, sym_stride, stage, tile);
   __syncthreads();
 
   // Two streams per step (st and st + kEncWaves), so their LDS round trips
@@ -583,6 +603,223 @@ __global__ void __launch_bounds__(kEncTileThreads)
       }
       if (lane == 0) lens[s0 + stv[j]] = static_cast<int32_t>(tbytes);
     }
+  }
+}
+
+// Split encode (T <= 256, a full block of 64 channels): 64 streams per
+// block and PIECES waves, wave w taking tokens [w * Q, (w + 1) * Q) of every
+// stream (Q = 256 / PIECES), lane s stream s.  Each lane walks a serial
+// chain of only Q codes, and every wave instruction works for 64 streams.
+//   1. The block's CDF rows (contiguous in memory) are staged with dword
+//      loads; its symbols are staged untransposed, [token][64 channels]
+//      bytes, with 16-byte stores (tokens T .. 255 read as 0xFF, not
+//      coded).  Lane s then reads token t's symbol at t * 64 + s: the 64
+//      lanes read 16 consecutive words.
+//   2. Code table in LDS, [symbol][stream] words of (code << 11) | length
+//      (rules L1-L3), built with lane = stream, so its stores and the
+//      lookups of step 3 each hit 64 distinct banks; row nb is all zeros
+//      and takes every symbol >= nb.  Wave w writes the w-th share of the
+//      symbols, after finding from the row whether the wrap of rule L2
+//      (an entry below its predecessor) lies before its share.  The block
+//      notes whether any code is longer than 8 bits.
+//   3. Each lane looks up its Q codes into registers and sums their
+//      lengths (the sum of the entries' low 11 bits: at most 64 x 15 bits,
+//      so no carry reaches the code field).  The piece lengths of a stream
+//      give each piece its bit offset.
+//   4. The staged data is dead; the same LDS holds one zeroed bit row per
+//      stream (2T bytes + a word: codes are at most 15 bits), and each lane
+//      ORs its codes in as runs of at most 32 bits: four codes per run when
+//      no code of the block is longer than 8 bits, else two.
+//   5. Rows leave as in the wave encoder: wave w stores the rows of streams
+//      w, w + PIECES, ..., lane k word k, only bytes below
+//      min(chunk, stream length).
+template <int PIECES>
+__device__ __forceinline__ void enc_append(uint32_t *brow, uint32_t &pos, uint32_t run, uint32_t n) {
+  // `run` holds n <= 32 bits (0 when n is 0); its top-aligned form is ORed
+  // into the one or two words it touches.
+  const uint32_t top = run << ((32u - n) & 31u);
+  const uint32_t wi = pos >> 5, sh = pos & 31u;
+  atomicOr(brow + wi, top >> sh);  // a no-op when n is 0
+  if (sh + n > 32u) atomicOr(brow + wi + 1, top << (32u - sh));
+  pos += n;
+}
+
+template <int PIECES>
+__global__ void __launch_bounds__(64 * PIECES)
+    encode_split_kernel(const int16_t *__restrict__ cdf,
+                        const uint8_t *__restrict__ in, int T, int C, int nb,
+                        uint8_t *__restrict__ out, int64_t chunk,
+                        int32_t *__restrict__ lens, int tiles, int word_stores, int row_words,
+                        int stage_words) {
+  constexpr int NT = 64 * PIECES;
+  constexpr int Q = kEncTileMaxT / PIECES;  // tokens per piece
+  // Phase 1: [64][nb + 1] int16 rows | [256][64] u8 symbols | [nb + 1][64] u32 codes
+  // Phase 2: [64][row_words] u32 bit rows (over phase 1)
+  // Always:  [PIECES][64] u32 piece lengths, then the long-code flag, after both
+  extern __shared__ uint32_t lds[];
+  typedef unsigned int w4 __attribute__((ext_vector_type(4)));
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l = blockIdx.x / tiles;
+  const int c0 = (blockIdx.x % tiles) * kEncLanes;
+  const int64_t s0 = static_cast<int64_t>(l) * C + c0;
+  const int rows_words = ((nb + 1) * kEncLanes * 2 + 15) / 16 * 4;
+  int16_t *stage = reinterpret_cast<int16_t *>(lds);
+  uint8_t *tile = reinterpret_cast<uint8_t *>(lds + rows_words);
+  uint32_t *tab = lds + rows_words + kEncTileMaxT * kEncLanes / 4;
+  uint32_t *bits = lds;
+  uint32_t *plen = lds + stage_words;
+  uint32_t *long_flag = plen + PIECES * kEncLanes;
+
+  // 1. Staging: every global load of the thread, then its LDS stores.  The
+  //    block's rows start at an even entry (s0 is a multiple of 64) and hold
+  //    an even number of entries, so they are whole dwords.
+  {
+    const uint32_t *rsrc = reinterpret_cast<const uint32_t *>(cdf + s0 * (nb + 1));
+    const int rcount = kEncLanes * (nb + 1) / 2;
+    constexpr int kR = (kEncLanes * 33 / 2 + NT - 1) / NT;  // row dwords per thread for nb <= 32
+    uint32_t rv[kR];
+    int ri[kR];
+#pragma unroll
+    for (int k = 0; k < kR; ++k) {
+      const int i = k * NT + tid;
+      ri[k] = i < rcount ? i : rcount - 1;
+      rv[k] = rsrc[ri[k]];
+    }
+    const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
+    constexpr int kV = (4 * kEncTileMaxT + NT - 1) / NT;  // 16-byte pieces per thread
+    const int pieces = T * 4;
+    w4 v[kV];
+    int pi[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int i = k * NT + tid;
+      pi[k] = i < pieces ? i : pieces - 1;
+      v[k] = *reinterpret_cast<const w4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16);
+    }
+    const w4 none = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int i = k * NT + tid;  // every piece of the 256 x 64 tile, in or past T
+      reinterpret_cast<w4 *>(tile)[i] = i < pieces ? v[k] : none;
+    }
+    uint32_t *rdst = reinterpret_cast<uint32_t *>(stage);
+#pragma unroll
+    for (int k = 0; k < kR; ++k) rdst[ri[k]] = rv[k];
+    for (int i = kR * NT + tid; i < rcount; i += NT) rdst[i] = rsrc[i];
+    if (tid == 0) *long_flag = 0u;
+  }
+  __syncthreads();
+
+  // 2. Code table, lane = stream; wave w writes symbols [j0, j1).
+  {
+    const int16_t *row = stage + lane * (nb + 1);
+    const int share = (nb + PIECES - 1) / PIECES;
+    const int j0 = wv * share;
+    const int j1 = j0 + share < nb ? j0 + share : nb;
+    // wrapped: some entry before j0 (j >= 1) lies below its predecessor.
+    bool wrapped = false;
+    uint32_t prev = static_cast<uint16_t>(row[0]) & 0xFFF0u;
+    for (int j = 1; j <= j0 && j < nb; ++j) {
+      const uint32_t cur = static_cast<uint16_t>(row[j]) & 0xFFF0u;
+      wrapped = wrapped || cur < prev;
+      prev = cur;
+    }
+    uint32_t longest = 0;
+    uint32_t raw = static_cast<uint16_t>(row[j0 < nb ? j0 : 0]);
+    for (int j = j0; j < j1; ++j) {
+      const uint32_t raw_n = j + 1 < nb ? static_cast<uint16_t>(row[j + 1]) : 0u;
+      const uint32_t base = wrapped ? 0x10000u : (raw & 0xFFF0u);
+      const bool wrapped_n = wrapped || (j + 1 < nb && (raw_n & 0xFFF0u) < (raw & 0xFFF0u));
+      const uint32_t next = (j + 1 < nb && !wrapped_n) ? (raw_n & 0xFFF0u) : 0x10000u;
+      const uint32_t width = next - base;
+      // Rule L3: the low bits, else 16 - floor(log2(width)) (0 for an empty interval).
+      const uint32_t wlen = width ? static_cast<uint32_t>(__builtin_clz(width)) - 15u : 0u;
+      const uint32_t len = (raw & 0xFu) ? (raw & 0xFu) : wlen;
+      const uint32_t code = __builtin_amdgcn_ubfe(base, kPrec - len, len);  // 0 when len is 0
+      tab[j * kEncLanes + lane] = (code << 11) | len;
+      longest = len > longest ? len : longest;
+      wrapped = wrapped_n;
+      raw = raw_n;
+    }
+    if (wv == 0) tab[nb * kEncLanes + lane] = 0u;
+    if (__ballot(longest > 8u) && lane == 0) *long_flag = 1u;
+  }
+  __syncthreads();
+  const bool long_codes = *long_flag != 0u;
+
+  // 3. Lookups into registers, and the piece's length.
+  uint32_t e[Q];
+  uint32_t sum = 0;
+  {
+    const uint8_t *scol = tile + wv * Q * kEncLanes + lane;
+    const uint32_t *tcol = tab + lane;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t v = scol[i * kEncLanes];
+      e[i] = tcol[(v < static_cast<uint32_t>(nb) ? v : static_cast<uint32_t>(nb)) * kEncLanes];
+    }
+#pragma unroll
+    for (int i = 0; i < Q; i += 2) sum += e[i] + e[i + 1];
+  }
+  plen[wv * kEncLanes + lane] = sum & 0x7FFu;
+  __syncthreads();
+
+  // 4. Bit rows: zeroed, then each piece ORed in at its offset.
+  {
+    const int n4 = (kEncLanes * row_words) / 4;
+    w4 *b4 = reinterpret_cast<w4 *>(bits);
+    const w4 z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < n4; i += NT) b4[i] = z;
+    for (int i = 4 * n4 + tid; i < kEncLanes * row_words; i += NT) bits[i] = 0u;
+  }
+  uint32_t pos = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < PIECES; ++w) {
+    const uint32_t n = plen[w * kEncLanes + lane];
+    pos += w < wv ? n : 0u;
+    total += n;
+  }
+  __syncthreads();
+  {
+    uint32_t *brow = bits + lane * row_words;
+    if (!long_codes) {
+      // Codes of at most 8 bits: four to a run.
+#pragma unroll
+      for (int i = 0; i < Q; i += 4) {
+        uint32_t run = e[i] >> 11;
+        run = (run << (e[i + 1] & 31u)) | (e[i + 1] >> 11);
+        run = (run << (e[i + 2] & 31u)) | (e[i + 2] >> 11);
+        run = (run << (e[i + 3] & 31u)) | (e[i + 3] >> 11);
+        const uint32_t n = (e[i] + e[i + 1] + e[i + 2] + e[i + 3]) & 0x7FFu;
+        enc_append<PIECES>(brow, pos, run, n);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < Q; i += 2) {
+        const uint32_t run = ((e[i] >> 11) << (e[i + 1] & 31u)) | (e[i + 1] >> 11);
+        const uint32_t n = (e[i] + e[i + 1]) & 0x7FFu;  // <= 30
+        enc_append<PIECES>(brow, pos, run, n);
+      }
+    }
+  }
+  if (wv == 0) lens[s0 + lane] = static_cast<int32_t>((total + 7) >> 3);
+  __syncthreads();
+
+  // 5. The rows: full words as dword stores, the bytes of a last partial
+  //    word by one lane each (a stream is at most 2T + 1 <= 513 bytes).
+  for (int st = wv; st < kEncLanes; st += PIECES) {
+    const uint32_t tb = __builtin_amdgcn_readlane(static_cast<int>(total), st);  // wave-uniform
+    const uint32_t tbytes = (tb + 7) >> 3;
+    const uint32_t nbytes = chunk < static_cast<int64_t>(tbytes) ? static_cast<uint32_t>(chunk) : tbytes;
+    uint8_t *orow = out + (s0 + st) * chunk;
+    const uint32_t *brow = bits + st * row_words;
+    const uint32_t nw = word_stores ? nbytes >> 2 : 0u;
+    for (uint32_t k = lane; k < nw; k += kEncLanes)
+      reinterpret_cast<uint32_t *>(orow)[k] = __builtin_bswap32(brow[k]);
+    for (uint32_t b = 4 * nw + lane; b < nbytes; b += kEncLanes)
+      orow[b] = static_cast<uint8_t>(brow[b >> 2] >> (24 - 8 * (b & 3u)));
   }
 }
 
@@ -1341,6 +1578,28 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
     const int tiles = static_cast<int>((C + kEncLanes - 1) / kEncLanes);
     const int word_stores =
         (chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(ob.data) & 3) == 0) ? 1 : 0;
+    const int vec_in = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
+    const bool rows_dw = (reinterpret_cast<uintptr_t>(cdf.data) & 3) == 0;
+    if (LMC_ENC_SPLIT && T > 0 && T <= kEncTileMaxT && nb <= kEncLanes && C % kEncLanes == 0 && vec_in &&
+        rows_dw) {
+      // Split encoder: bit rows of 2T bytes plus one word (codes are at
+      // most 16 bits), an odd number of words so that the lanes' rows start
+      // in different banks.
+      const int row_words = (static_cast<int>(T + 1) / 2 + 1) | 1;
+      const int rows_words = static_cast<int>(((nb + 1) * kEncLanes * 2 + 15) / 16 * 4);
+      const int phase1 = rows_words + kEncTileMaxT * kEncLanes / 4 + static_cast<int>(nb + 1) * kEncLanes;
+      const int stage_words = std::max(phase1, kEncLanes * row_words);
+      const size_t lds = 4 * (static_cast<size_t>(stage_words) + kEncPieces * kEncLanes + 1);
+      check(lds <= 65536, "encode: LDS budget exceeded");
+      hipLaunchKernelGGL(encode_split_kernel<kEncPieces>, dim3(L * tiles), dim3(64 * kEncPieces), lds,
+                         static_cast<hipStream_t>(stream),
+                         static_cast<const int16_t *>(cdf.data),
+                         static_cast<const uint8_t *>(in.data), (int)T, (int)C,
+                         (int)nb, static_cast<uint8_t *>(ob.data), chunk,
+                         static_cast<int32_t *>(ol.data), tiles, word_stores, row_words, stage_words);
+      hip_check(hipGetLastError(), "encode_split_kernel launch");
+      return;
+    }
     if (T > 0 && T <= kEncTileMaxT && nb <= kEncLanes) {
       // Bits past min(chunk, 2 bytes per symbol) are never written (codes
       // are at most 16 bits), so a wave's bit buffer holds that many bytes.
@@ -1350,7 +1609,7 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
       const size_t lds = 4 * ((static_cast<size_t>(nb + 1) * kEncLanes * 2 + 15) / 16 * 4 +
                               static_cast<size_t>(kEncLanes) * sym_stride +
                               static_cast<size_t>(2 * kEncWaves) * cap_words);
-      const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
+      const int vec_tile = vec_in;
       check(lds <= 65536, "encode: LDS budget exceeded");
       hipLaunchKernelGGL(encode_wave_kernel, dim3(L * tiles), dim3(kEncTileThreads), lds,
                          static_cast<hipStream_t>(stream),

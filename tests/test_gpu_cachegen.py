@@ -263,6 +263,28 @@ def test_decode_arbitrary_cdf_rows_vs_oracle(ops, nb, step):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("nb", [2, 17, 32, 33, 64])
+@pytest.mark.parametrize("T,C,chunk", [(256, 128, 600), (256, 64, 37), (130, 192, 300), (7, 64, 16), (1, 128, 5)])
+def test_encode_arbitrary_cdf_rows_vs_oracle(ops, nb, T, C, chunk):
+    """Encode under hand-built CDF rows (codes of 1 to 15 bits, wrapped
+    rows, absent symbols) of random symbols, some of them >= n_bins, against
+    the oracle: byte lengths, and every output byte including the untouched
+    guard bytes past each stream and past short rows (chunk 37 and 5 are
+    not multiples of 4; chunk 37, 16 and 5 truncate streams)."""
+    rng = np.random.default_rng(300 + nb + T + C + chunk)
+    L = 2
+    cdf = _arbitrary_cdf_rows(rng, L, C, nb, 16)
+    syms = rng.integers(0, nb + 3, size=(L, T, C)).astype(np.uint8)
+    guard = np.full((L, C, chunk), 0xEE, np.uint8)
+    out = torch.from_numpy(guard.copy()).to(DEV)
+    lens = torch.zeros((L, C), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(torch.from_numpy(cdf).to(DEV), torch.from_numpy(syms).to(DEV), out, lens)
+    want_out, want_len = oc.encode(cdf, syms, chunk, out=guard.copy())
+    torch.cuda.synchronize()
+    assert np.array_equal(lens.cpu().numpy(), want_len)
+    assert np.array_equal(out.cpu().numpy(), want_out)
+
+
 @pytest.mark.parametrize("T", [5, 256])
 def test_decode_random_streams_under_calculated_cdfs(ops, T):
     """Tables from calculate_cdf on 256-token chunks hold no escape entry,
