@@ -187,11 +187,15 @@ constexpr int kCdfWaves = 4;
 constexpr int kCdfThreads = 64 * kCdfWaves;
 constexpr int kCdfMaxT = 256;
 
-template <int kBins>  // register capacity for code lengths: nb <= kBins
+// kBins: register capacity for code lengths (nb <= kBins); kExact: nb ==
+// kBins, so every per-symbol bound is a constant.
+template <int kBins, bool kExact>
 __global__ void __launch_bounds__(kCdfThreads)
     cdf_tile_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
                     int16_t *__restrict__ out, int tiles, int vec_tile) {
-  // [T][64] u8 symbols | [nb][64] u32 histogram | [64][nb + 1] int16 rows
+  if (kExact) nb = kBins;
+  // [T][64] u8 symbols | [nb][64] u32 histogram | [64] u32 counts | [64] u32
+  // Kraft sums | [64][nb + 1] int16 rows
   extern __shared__ uint32_t lds[];
   const int tid = static_cast<int>(threadIdx.x);
   const int q = tid / 64;
@@ -202,8 +206,10 @@ __global__ void __launch_bounds__(kCdfThreads)
   uint8_t *tile = reinterpret_cast<uint8_t *>(lds);
   const int tile_words = (T * 64 + 15) / 16 * 4;
   uint32_t *hist = lds + tile_words;
-  int16_t *rows = reinterpret_cast<int16_t *>(hist + nb * 64);
-  for (int i = tid; i < nb * 64; i += kCdfThreads) hist[i] = 0;
+  uint32_t *nsum = hist + nb * 64;   // per stream: symbol count
+  uint32_t *ksum = nsum + 64;        // per stream: Kraft sum (units of 2^-16)
+  int16_t *rows = reinterpret_cast<int16_t *>(ksum + 64);
+  for (int i = tid; i < nb * 64 + 128; i += kCdfThreads) hist[i] = 0;
   const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
   const int pieces = T * 4;
   if (vec_tile && cnt == 64) {
@@ -227,79 +233,116 @@ __global__ void __launch_bounds__(kCdfThreads)
   const int Tq = (T + kCdfWaves - 1) / kCdfWaves;
   const int tb = q * Tq < T ? q * Tq : T;
   const int te = tb + Tq < T ? tb + Tq : T;
-  if (lane < cnt) {
-    for (int t0 = tb; t0 < te; t0 += kBatch) {
+  if (lane < cnt && tb < te) {
+    // Symbols that are not counted add 0 to row 0 (no branch per symbol).
+    const int tq = te - tb;
+    const uint8_t *scol = tile + tb * 64 + lane;
+    for (int t0 = 0; t0 < tq; t0 += kBatch) {
       uint32_t sym[kBatch];
+      if (t0 + kBatch <= tq) {
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) sym[i] = t0 + i < te ? tile[(t0 + i) * 64 + lane] : 0xFFu;
+        for (int i = 0; i < kBatch; ++i) sym[i] = scol[(t0 + i) * 64];
+      } else {
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i)
-        if (sym[i] < static_cast<uint32_t>(nb)) atomicAdd(&hist[sym[i] * 64 + lane], 1u);
+        for (int i = 0; i < kBatch; ++i) sym[i] = t0 + i < tq ? scol[(t0 + i) * 64] : 0xFFu;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const bool ok = sym[i] < static_cast<uint32_t>(nb);
+        atomicAdd(&hist[(ok ? sym[i] : 0u) * 64 + lane], ok ? 1u : 0u);
+      }
     }
   }
   __syncthreads();
-  if (q == 0 && lane < cnt) {
-    const uint32_t *col = hist + lane;
-    uint32_t n = 0;
+  // Derivation, spread over the waves: wave q takes symbols [j0, j1) of
+  // every stream (lane = stream) for the count sums, the code lengths and
+  // the Kraft sums; one wave per block, rotating with the block index so
+  // that the blocks of a CU use different SIMDs, then makes the serial
+  // aligned assignment.
+  constexpr int kS = kBins / kCdfWaves;
+  const int share = (nb + kCdfWaves - 1) / kCdfWaves;
+  const int j0 = q * share;
+  const int j1 = j0 + share < nb ? j0 + share : nb;
+  uint32_t cnt_j[kS];
+  {
+    uint32_t part = 0;
 #pragma unroll
-    for (int s = 0; s < kBins; ++s) n += s < nb ? col[s * 64] : 0u;
-    uint32_t len[kBins];
-    uint32_t kraft = 0;  // units of 2^-16
+    for (int k = 0; k < kS; ++k) {
+      cnt_j[k] = (k < share && j0 + k < j1) ? hist[(j0 + k) * 64 + lane] : 0u;
+      part += cnt_j[k];
+    }
+    if (lane < cnt && part) atomicAdd(nsum + lane, part);
+  }
+  __syncthreads();
+  {
+    const uint32_t n = nsum[lane];
     const int ln = 31 - __builtin_clz(n | 1u);
+    uint32_t kpart = 0;  // units of 2^-16
 #pragma unroll
-    for (int s = 0; s < kBins; ++s) {
-      const uint32_t cs = s < nb ? col[s * 64] : 0u;
+    for (int k = 0; k < kS; ++k) {
+      const uint32_t cs = cnt_j[k];
       uint32_t x = 0;
       if (cs) {
         x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs)));
         if ((static_cast<uint64_t>(cs) << x) < n) ++x;
         x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
-        kraft += 1u << (kPrec - x);
+        kpart += 1u << (kPrec - x);
       }
-      len[s] = x;
+      if (k < share && j0 + k < j1) hist[(j0 + k) * 64 + lane] = (x << 16) | cs;
+    }
+    if (lane < cnt && kpart) atomicAdd(ksum + lane, kpart);
+  }
+  __syncthreads();
+  if (q == static_cast<int>(blockIdx.x % kCdfWaves) && lane < cnt) {
+    const uint32_t *col = hist + lane;  // (length << 16) | count
+    uint32_t len[kBins];
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) {
+      const uint32_t v = col[(s < nb ? s : 0) * 64];  // every read issued before the first use
+      len[s] = s < nb ? v >> 16 : 0u;
     }
     // Kraft repair: lengthen the rarest present symbol below the cap (the
-    // last one among equals) until the code fits.
-    while (kraft > (1u << kPrec)) {
-      int pick = -1;
-      uint32_t best = 0;
-#pragma unroll
-      for (int s = 0; s < kBins; ++s) {
-        const uint32_t cs = s < nb ? col[s * 64] : 0u;
-        if (len[s] != 0 && len[s] < kMaxLen && (pick < 0 || cs <= best)) {
-          pick = s;
-          best = cs;
+    // last one among equals) until the code fits.  Never needed for T <=
+    // 256 (no Shannon length reaches the cap), so it runs out of line on
+    // the LDS copy of (length, count) and is kept out of the unrolled code.
+    uint32_t kraft = ksum[lane];
+    if (kraft > (1u << kPrec)) {
+      uint32_t *wcol = hist + lane;
+      while (kraft > (1u << kPrec)) {
+        int pick = -1;
+        uint32_t best = 0;
+#pragma unroll 1
+        for (int s = 0; s < nb; ++s) {
+          const uint32_t v = wcol[s * 64], ls = v >> 16, cs = v & 0xFFFFu;
+          if (ls != 0 && ls < kMaxLen && (pick < 0 || cs <= best)) {
+            pick = s;
+            best = cs;
+          }
         }
+        if (pick < 0) break;
+        const uint32_t lp = wcol[pick * 64] >> 16;
+        kraft -= 1u << (kPrec - lp - 1);
+        wcol[pick * 64] += 1u << 16;
       }
-      if (pick < 0) break;
 #pragma unroll
-      for (int s = 0; s < kBins; ++s)
-        if (s == pick) {
-          kraft -= 1u << (kPrec - len[s] - 1);
-          ++len[s];
-        }
+      for (int s = 0; s < kBins; ++s) len[s] = s < nb ? col[s * 64] >> 16 : 0u;
     }
     // Aligned in-order assignment.  A symbol's base is the running position
-    // `pos`; an absent symbol (length 0) gets the same value, which is the
-    // base of the next present symbol (or the end).
+    // `pos`, its width 2^(16 - length) capped by the lowest set bit of `pos`
+    // (the code lengthened to match); an absent symbol (length 0) gets the
+    // same value, which is the base of the next present symbol (or the end).
     int16_t *row = rows + lane * (nb + 1);
     uint32_t pos = 0;
 #pragma unroll
     for (int s = 0; s < kBins; ++s) {
       if (s < nb) {
-        uint32_t x = len[s];
-        if (x) {
-          uint32_t w = 1u << (kPrec - x);
-          const uint32_t low = pos & (0u - pos);  // lowest set bit (0 when pos == 0)
-          if (low && low < w) {
-            x += (31 - __builtin_clz(w)) - (31 - __builtin_clz(low));
-            w = low;
-          }
-          row[s] = static_cast<int16_t>(static_cast<uint16_t>((pos | x) & 0xFFFFu));
-          pos += w;
-        } else {
-          row[s] = static_cast<int16_t>(static_cast<uint16_t>(pos & 0xFFFFu));
-        }
+        const uint32_t x0 = len[s];
+        const uint32_t w0 = x0 ? 1u << (kPrec - x0) : 0u;
+        const uint32_t low = pos & (0u - pos);  // lowest set bit (0 when pos == 0)
+        const bool shrink = low != 0 && low < w0;
+        const uint32_t x = shrink ? x0 + static_cast<uint32_t>(__builtin_clz(low) - __builtin_clz(w0)) : x0;
+        row[s] = static_cast<int16_t>(static_cast<uint16_t>((pos | x) & 0xFFFFu));
+        pos += shrink ? low : w0;
       }
     }
     row[nb] = 0;
@@ -655,7 +698,8 @@ __global__ void __launch_bounds__(64 * PIECES)
   constexpr int Q = kEncTileMaxT / PIECES;  // tokens per piece
   // Phase 1: [64][nb + 1] int16 rows | [256][64] u8 symbols | [nb + 1][64] u32 codes
   // Phase 2: [64][row_words] u32 bit rows (over phase 1)
-  // Always:  [PIECES][64] u32 piece lengths, then the long-code flag, after both
+  // Always:  [PIECES][64] u32 piece lengths, the long-code flag and [64] u64
+  //          decrease masks, after both
   extern __shared__ uint32_t lds[];
   typedef unsigned int w4 __attribute__((ext_vector_type(4)));
   const int tid = static_cast<int>(threadIdx.x);
@@ -671,6 +715,7 @@ __global__ void __launch_bounds__(64 * PIECES)
   uint32_t *bits = lds;
   uint32_t *plen = lds + stage_words;
   uint32_t *long_flag = plen + PIECES * kEncLanes;
+  uint64_t *dmask = reinterpret_cast<uint64_t *>(lds + ((stage_words + PIECES * kEncLanes + 2) & ~1));
 
   // 1. Staging: every global load of the thread, then its LDS stores.  The
   //    block's rows start at an even entry (s0 is a multiple of 64) and hold
@@ -709,39 +754,54 @@ __global__ void __launch_bounds__(64 * PIECES)
     for (int k = 0; k < kR; ++k) rdst[ri[k]] = rv[k];
     for (int i = kR * NT + tid; i < rcount; i += NT) rdst[i] = rsrc[i];
     if (tid == 0) *long_flag = 0u;
+    if (tid < kEncLanes) dmask[tid] = 0u;
   }
   __syncthreads();
 
-  // 2. Code table, lane = stream; wave w writes symbols [j0, j1).
+  // 2. Code table, lane = stream; wave w writes symbols [j0, j1).  First
+  //    each wave marks the decreases of rule L2 in its range (entry j below
+  //    entry j - 1) in the stream's 64-bit mask, so that afterwards symbol j
+  //    is wrapped exactly when the mask has a bit at or below j.
   {
+    constexpr int kShare = (kMaxBins + PIECES - 1) / PIECES;
     const int16_t *row = stage + lane * (nb + 1);
     const int share = (nb + PIECES - 1) / PIECES;
     const int j0 = wv * share;
     const int j1 = j0 + share < nb ? j0 + share : nb;
-    // wrapped: some entry before j0 (j >= 1) lies below its predecessor.
-    bool wrapped = false;
-    uint32_t prev = static_cast<uint16_t>(row[0]) & 0xFFF0u;
-    for (int j = 1; j <= j0 && j < nb; ++j) {
-      const uint32_t cur = static_cast<uint16_t>(row[j]) & 0xFFF0u;
-      wrapped = wrapped || cur < prev;
-      prev = cur;
+    uint32_t m[kShare + 1];  // masked entries j0 .. j0 + kShare (0 past nb - 1)
+#pragma unroll
+    for (int k = 0; k <= kShare; ++k)
+      m[k] = (k <= share && j0 + k < nb) ? (static_cast<uint16_t>(row[j0 + k]) & 0xFFF0u) : 0u;
+    const uint32_t m_before = j0 > 0 && j0 < nb ? (static_cast<uint16_t>(row[j0 - 1]) & 0xFFF0u) : 0u;
+    uint64_t dec = 0;
+#pragma unroll
+    for (int k = 0; k < kShare; ++k) {
+      const int jj = j0 + k;
+      const uint32_t prev = k == 0 ? m_before : m[k - 1];
+      if (k < share && jj < j1 && jj >= 1 && m[k] < prev) dec |= uint64_t(1) << jj;
     }
+    if (dec) atomicOr(dmask + lane, static_cast<unsigned long long>(dec));
+    __syncthreads();
+    const uint64_t D = dmask[lane];
     uint32_t longest = 0;
-    uint32_t raw = static_cast<uint16_t>(row[j0 < nb ? j0 : 0]);
-    for (int j = j0; j < j1; ++j) {
-      const uint32_t raw_n = j + 1 < nb ? static_cast<uint16_t>(row[j + 1]) : 0u;
-      const uint32_t base = wrapped ? 0x10000u : (raw & 0xFFF0u);
-      const bool wrapped_n = wrapped || (j + 1 < nb && (raw_n & 0xFFF0u) < (raw & 0xFFF0u));
-      const uint32_t next = (j + 1 < nb && !wrapped_n) ? (raw_n & 0xFFF0u) : 0x10000u;
-      const uint32_t width = next - base;
-      // Rule L3: the low bits, else 16 - floor(log2(width)) (0 for an empty interval).
-      const uint32_t wlen = width ? static_cast<uint32_t>(__builtin_clz(width)) - 15u : 0u;
-      const uint32_t len = (raw & 0xFu) ? (raw & 0xFu) : wlen;
-      const uint32_t code = __builtin_amdgcn_ubfe(base, kPrec - len, len);  // 0 when len is 0
-      tab[j * kEncLanes + lane] = (code << 11) | len;
-      longest = len > longest ? len : longest;
-      wrapped = wrapped_n;
-      raw = raw_n;
+#pragma unroll
+    for (int k = 0; k < kShare; ++k) {
+      const int jj = j0 + k;
+      if (k < share && jj < j1) {
+        const uint32_t raw = static_cast<uint16_t>(row[jj]);
+        const bool wrapped = (D & (~uint64_t(0) >> (63 - jj))) != 0;
+        const bool has_n = jj + 1 < nb;
+        const bool wrapped_n = has_n && (D & (~uint64_t(0) >> (62 - jj))) != 0;
+        const uint32_t base = wrapped ? 0x10000u : m[k];
+        const uint32_t next = (has_n && !wrapped_n) ? m[k + 1] : 0x10000u;
+        const uint32_t width = next - base;
+        // Rule L3: the low bits, else 16 - floor(log2(width)) (0 for an empty interval).
+        const uint32_t wlen = width ? static_cast<uint32_t>(__builtin_clz(width)) - 15u : 0u;
+        const uint32_t len = (raw & 0xFu) ? (raw & 0xFu) : wlen;
+        const uint32_t code = __builtin_amdgcn_ubfe(base, kPrec - len, len);  // 0 when len is 0
+        tab[jj * kEncLanes + lane] = (code << 11) | len;
+        longest = len > longest ? len : longest;
+      }
     }
     if (wv == 0) tab[nb * kEncLanes + lane] = 0u;
     if (__ballot(longest > 8u) && lane == 0) *long_flag = 1u;
@@ -1519,19 +1579,16 @@ int lmc_calculate_cdf(const lmc_tensor *input, int32_t n_bins,
     DeviceGuard guard(in.device);
     if (T >= 1 && T <= kCdfMaxT) {
       const int tiles64 = static_cast<int>((C + 63) / 64);
-      const size_t lds = 4 * (static_cast<size_t>((T * 64 + 15) / 16 * 4) + static_cast<size_t>(n_bins) * 64) +
+      const size_t lds = 4 * (static_cast<size_t>((T * 64 + 15) / 16 * 4) + static_cast<size_t>(n_bins) * 64 + 128) +
                          static_cast<size_t>(64) * (n_bins + 1) * 2;
       const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
-      if (n_bins <= 32)
-        hipLaunchKernelGGL(cdf_tile_kernel<32>, dim3(L * tiles64), dim3(kCdfThreads), lds,
-                           static_cast<hipStream_t>(stream),
-                           static_cast<const uint8_t *>(in.data), (int)T, (int)C,
-                           n_bins, static_cast<int16_t *>(o.data), tiles64, vec_tile);
-      else
-        hipLaunchKernelGGL(cdf_tile_kernel<kMaxBins>, dim3(L * tiles64), dim3(kCdfThreads), lds,
-                           static_cast<hipStream_t>(stream),
-                           static_cast<const uint8_t *>(in.data), (int)T, (int)C,
-                           n_bins, static_cast<int16_t *>(o.data), tiles64, vec_tile);
+      const auto kern = n_bins == 32         ? cdf_tile_kernel<32, true>
+                        : n_bins < 32          ? cdf_tile_kernel<32, false>
+                        : n_bins == kMaxBins   ? cdf_tile_kernel<kMaxBins, true>
+                                               : cdf_tile_kernel<kMaxBins, false>;
+      hipLaunchKernelGGL(kern, dim3(L * tiles64), dim3(kCdfThreads), lds, static_cast<hipStream_t>(stream),
+                         static_cast<const uint8_t *>(in.data), (int)T, (int)C, n_bins,
+                         static_cast<int16_t *>(o.data), tiles64, vec_tile);
       hip_check(hipGetLastError(), "cdf_tile_kernel launch");
       return;
     }
@@ -1589,7 +1646,7 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
       const int rows_words = static_cast<int>(((nb + 1) * kEncLanes * 2 + 15) / 16 * 4);
       const int phase1 = rows_words + kEncTileMaxT * kEncLanes / 4 + static_cast<int>(nb + 1) * kEncLanes;
       const int stage_words = std::max(phase1, kEncLanes * row_words);
-      const size_t lds = 4 * (static_cast<size_t>(stage_words) + kEncPieces * kEncLanes + 1);
+      const size_t lds = 4 * (static_cast<size_t>((stage_words + kEncPieces * kEncLanes + 2) & ~1) + 2 * kEncLanes);
       check(lds <= 65536, "encode: LDS budget exceeded");
       hipLaunchKernelGGL(encode_split_kernel<kEncPieces>, dim3(L * tiles), dim3(64 * kEncPieces), lds,
                          static_cast<hipStream_t>(stream),
