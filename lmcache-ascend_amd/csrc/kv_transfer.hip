@@ -101,6 +101,7 @@ using ChunkList = ChunkListT<kMaxChunks>;
 
 // Resolves row `row` of chunk `c` to (src, dst); returns the row's byte count,
 // or 0 when the slot is skipped.  All inputs are wave-uniform.
+template <bool SLOT32, bool TABLE>
 __device__ __forceinline__ int64_t row_ptrs(const CopyJob &job, uint8_t *lmc,
                                             int tok0, int T, int per_plane,
                                             int row, const uint8_t *&src,
@@ -109,28 +110,16 @@ __device__ __forceinline__ int64_t row_ptrs(const CopyJob &job, uint8_t *lmc,
   const int rem = row - p * per_plane;
   const int l = rem / T;
   const int t = rem - l * T;
-  int64_t slot = job.slot_i32
-                     ? static_cast<int64_t>(
-                           static_cast<const int32_t *>(job.slots)[tok0 + t])
-                     : static_cast<const int64_t *>(job.slots)[tok0 + t];
-  slot = __builtin_amdgcn_readfirstlane(static_cast<int>(slot)) |
-         (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
-              static_cast<int>(slot >> 32)))
-          << 32);
+  // Independent loads, issued together: the slot and the plane's paged base
+  // (the empty asm takes both as scalar operands, so one wait covers both
+  // and the range check does not sit between them).
+  const int64_t slot = SLOT32 ? static_cast<int64_t>(static_cast<const int32_t *>(job.slots)[tok0 + t])
+                              : static_cast<const int64_t *>(job.slots)[tok0 + t];
+  const uint64_t pbase =
+      TABLE ? job.table[static_cast<int64_t>(l) * job.table_ppl + job.table_idx[p]] : job.base[p];
+  asm volatile("" ::"s"(slot), "s"(pbase));
   if (slot < 0 || slot >= job.num_slots) return 0;
   const PlaneDesc &pd = job.plane[p];
-  uint64_t pbase;
-  if (job.table != nullptr) {
-    pbase = job.table[static_cast<int64_t>(l) * job.table_ppl +
-                      job.table_idx[p]];
-    pbase = static_cast<uint32_t>(
-                __builtin_amdgcn_readfirstlane(static_cast<int>(pbase))) |
-            (static_cast<uint64_t>(static_cast<uint32_t>(
-                 __builtin_amdgcn_readfirstlane(static_cast<int>(pbase >> 32))))
-             << 32);
-  } else {
-    pbase = job.base[p];
-  }
   int64_t poff = pd.paged_off;
   if (job.block_size > 0) {
     const uint32_t s32 = static_cast<uint32_t>(slot);
@@ -160,7 +149,7 @@ __device__ __forceinline__ int64_t row_ptrs(const CopyJob &job, uint8_t *lmc,
 // (2 KiB with 16-byte accesses, a whole row at the Llama-3-8B shape).  A
 // wave owns kRowsPerWave items per pass: it resolves their addresses with
 // scalar work, issues every load, then every store.
-template <int VEC, bool NT, int NC>
+template <int VEC, bool NT, int NC, bool SLOT32, bool TABLE>
 __global__ void __launch_bounds__(kThreads)
     kv_rows_copy(const CopyJob job, const ChunkListT<NC> chunks) {
   using V = typename VecOf<VEC>::T;
@@ -197,7 +186,7 @@ __global__ void __launch_bounds__(kThreads)
       if (item < items) {
         const int row = item / spr;
         off0[r] = static_cast<int64_t>(item - row * spr) * kSlice;
-        nb[r] = row_ptrs(job, lmc, tok0, T, per_plane, row, src[r], dst[r]);
+        nb[r] = row_ptrs<SLOT32, TABLE>(job, lmc, tok0, T, per_plane, row, src[r], dst[r]);
       }
       // The host checked every alignment it can see; a table entry (a device
       // value) that is not VEC-aligned sends the item to the byte path.
@@ -520,6 +509,25 @@ ChunkListT<1> first_chunk(const ChunkList &cl) {
   return one;
 }
 
+template <int VEC, int NC, bool SLOT32, bool TABLE>
+void launch_rows_st(const CopyJob &job, const ChunkListT<NC> &chunks, dim3 grid, dim3 block, bool nt,
+                    hipStream_t stream) {
+  if (nt) hipLaunchKernelGGL((kv_rows_copy<VEC, true, NC, SLOT32, TABLE>), grid, block, 0, stream, job, chunks);
+  else hipLaunchKernelGGL((kv_rows_copy<VEC, false, NC, SLOT32, TABLE>), grid, block, 0, stream, job, chunks);
+}
+
+template <int VEC, int NC>
+void launch_rows(const CopyJob &job, const ChunkListT<NC> &chunks, dim3 grid, dim3 block, bool nt,
+                 hipStream_t stream) {
+  if (job.slot_i32) {
+    if (job.table != nullptr) launch_rows_st<VEC, NC, true, true>(job, chunks, grid, block, nt, stream);
+    else launch_rows_st<VEC, NC, true, false>(job, chunks, grid, block, nt, stream);
+  } else {
+    if (job.table != nullptr) launch_rows_st<VEC, NC, false, true>(job, chunks, grid, block, nt, stream);
+    else launch_rows_st<VEC, NC, false, false>(job, chunks, grid, block, nt, stream);
+  }
+}
+
 template <bool NT, int NC, bool TABLE, bool SLOT32>
 void launch_lean_p(const CopyJob &job, const ChunkListT<NC> &chunks, dim3 grid,
                    hipStream_t stream) {
@@ -608,17 +616,8 @@ void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
     const int items_per_block = kWaves * kRowsPerWave;
     int gx = static_cast<int>((max_items + items_per_block - 1) / items_per_block);
     dim3 grid(std::max(1, std::min(gx, LMC_KV_GRID_CAP)), n_chunks);
-    if (n_chunks == 1) {
-      const ChunkListT<1> one = first_chunk(chunks);
-      if (nt)
-        hipLaunchKernelGGL((kv_rows_copy<VEC, true, 1>), grid, block, 0, stream, job, one);
-      else
-        hipLaunchKernelGGL((kv_rows_copy<VEC, false, 1>), grid, block, 0, stream, job, one);
-    } else if (nt) {
-      hipLaunchKernelGGL((kv_rows_copy<VEC, true, kMaxChunks>), grid, block, 0, stream, job, chunks);
-    } else {
-      hipLaunchKernelGGL((kv_rows_copy<VEC, false, kMaxChunks>), grid, block, 0, stream, job, chunks);
-    }
+    if (n_chunks == 1) launch_rows<VEC>(job, first_chunk(chunks), grid, block, nt, stream);
+    else launch_rows<VEC>(job, chunks, grid, block, nt, stream);
   } else {
     // Narrower or odd rows: tiles of about 32 KiB of the widest plane,
     // 16..64 rows; a store between device buffers (paged reads) instead
