@@ -299,7 +299,8 @@ def bench_blend(torch, ops, dev, stream, flat, slots):
     earlier is scattered into the paged caches (single_layer_kv_transfer);
     a device-wide synchronize separates the steps and two buffers ping-pong.
     Also timed: the same work with three buffers ordered by events instead
-    of device-wide synchronizes, and each stage alone."""
+    of device-wide synchronizes, each stage alone, and the 32 layers through
+    blend_layer_to_paged (one kernel per layer, objects read in place)."""
     T = slots.numel()
     n_obj = T // CHUNK
     host = torch.randn((L, n_obj, 2, CHUNK, W), dtype=torch.float32).to(torch.bfloat16).pin_memory()
@@ -363,8 +364,25 @@ def bench_blend(torch, ops, dev, stream, flat, slots):
             ts.append((time.perf_counter() - t0) * 1e3)
         return statistics.median(ts)
 
+    # The same 32 layers through blend_layer_to_paged: one kernel per layer
+    # reads the layer's pinned objects in place, re-rotates K and scatters
+    # (no load buffer, no copy-engine copies).
+    objs = [[host[layer, c] for c in range(n_obj)] for layer in range(L)]
+    obj_starts = [c * CHUNK for c in range(n_obj)]
+
+    def fused_layers():
+        for layer in range(L):
+            ops.blend_layer_to_paged(objs[layer], obj_starts, (flat[2 * layer], flat[2 * layer + 1]), slots,
+                                     old_positions=old, new_positions=new, cos_sin_cache=cache, head_size=D,
+                                     is_neox=True, kvcache_format_raw=2)
+        torch.cuda.synchronize()
+
     t_ref = wall(reference_pattern)
     t_evt = wall(event_pipelined)
+    t_fused = wall(fused_layers)
+    t_fused_one = time_events(torch, stream, lambda: ops.blend_layer_to_paged(
+        objs[0], obj_starts, (flat[0], flat[1]), slots, old_positions=old, new_positions=new, cos_sin_cache=cache,
+        head_size=D, is_neox=True, kvcache_format_raw=2), 20)[0]
     with torch.cuda.stream(load_stream):
         t_h2d = time_events(torch, load_stream, lambda: h2d(bufs[0], 0), 10)[0]
     t_rope = time_events(torch, stream, lambda: rope(bufs[1]), 20)[0]
@@ -372,13 +390,18 @@ def bench_blend(torch, ops, dev, stream, flat, slots):
     layer_bytes = 2 * T * W * ES
     out = {}
     for name, t in (("blend_layerwise_reference_pattern_32_layers", t_ref),
-                    ("blend_layerwise_event_pipelined_32_layers", t_evt)):
+                    ("blend_layerwise_event_pipelined_32_layers", t_evt),
+                    ("blend_layer_to_paged_fused_32_layers", t_fused)):
         out[name] = {"ms": round(t, 4), "ms_per_layer": round(t / L, 4),
                      "payload_GBps": round(L * layer_bytes / (t * 1e-3) / 1e9, 2),
                      "pcie_frac": round(L * layer_bytes / (t * 1e-3) / 1e9 / PCIE_PEAK_GBS, 4)}
     out["blend_stage_h2d_16_objects_one_layer"] = {"ms": round(t_h2d, 4),
                                                    "payload_GBps": round(layer_bytes / (t_h2d * 1e-3) / 1e9, 2)}
     out["blend_stage_rope_one_layer"] = {"ms": round(t_rope, 4)}
+    out["blend_layer_to_paged_one_layer"] = {"ms": round(t_fused_one, 4),
+                                             "payload_GBps": round(layer_bytes / (t_fused_one * 1e-3) / 1e9, 2),
+                                             "pcie_frac": round(layer_bytes / (t_fused_one * 1e-3) / 1e9 / PCIE_PEAK_GBS,
+                                                                4)}
     out["blend_stage_scatter_one_layer"] = {"ms": round(t_scatter, 4),
                                             "hbm_GBps": round(2 * layer_bytes / (t_scatter * 1e-3) / 1e9, 1)}
     del host, bufs

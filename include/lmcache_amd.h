@@ -345,6 +345,29 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf,
  * Fused K re-rotation (CacheBlend)
  * ------------------------------------------------------------------------ */
 
+/* No counterpart in the reference: the CacheBlend connector's per-layer
+ * retrieve (lmcache_ascend/v1/npu_connector/npu_connectors.py:556-689) in one
+ * kernel.  The bytes written to the paged `caches` (MERGED_KV or SEPARATE_KV,
+ * one layer) equal the connector's sequence: a zeroed [2, N, W] buffer
+ * (N = slot_mapping.size(0)) receives each KV_2TD memory object
+ * `objects[i]` ([2, n_i, W]) at tokens [token_starts[i], token_starts[i] + n_i)
+ * (objects must not overlap); when positions are given, its K half is
+ * re-rotated as lmc_rotary_embedding_k_fused(old_positions, new_positions,
+ * K, head_size, cos_sin_cache, is_neox) would; the buffer is then scattered
+ * as lmc_single_layer_kv_transfer(buffer, caches, slot_mapping, 0, fmt, 0,
+ * vllm_two_major).  No buffer is allocated.  old_positions and
+ * new_positions are both null (no re-rotation) or both [N] device tensors.
+ * Objects may be device tensors or page-locked host memory (read in place).
+ * Geometry outside the kernel's (keys other than bf16/fp16, rows or heads
+ * not in 16-byte pieces, rotary halves not a multiple of 8 dims) returns
+ * LMC_ERR_NOT_IMPLEMENTED before any work. */
+int lmc_blend_layer_to_paged(const lmc_tensor *objects, int32_t n_objects,
+                             const int64_t *token_starts, const lmc_tensor *caches,
+                             int32_t n_caches, const lmc_tensor *slot_mapping,
+                             const lmc_tensor *old_positions, const lmc_tensor *new_positions,
+                             const lmc_tensor *cos_sin_cache, int64_t head_size, int32_t is_neox,
+                             int32_t kvcache_format, int32_t vllm_two_major, void *stream);
+
 /* Replaces rotary_embedding_k_fused (csrc/pos_kernels.cpp:158-196; pybind
  * csrc/pybind.cpp:481): key [T, H*head_size] is rotated in place from
  * old_positions to new_positions with the [max_pos, rot] cos|sin cache. */

@@ -21,48 +21,13 @@
 // head_size - rot dims pass through.  Tokens whose old or new position lies
 // outside the cache are left unchanged.
 #include "common.h"
+#include "rope_math.h"
 
 #include <cstring>
 
 namespace lmc {
 
 namespace {
-
-template <typename T, int N> struct alignas(sizeof(T) * N) Pack {
-  T v[N];
-};
-
-// Element storage types: bf16 and fp16 as raw 16-bit patterns.
-struct BF16 { using S = uint16_t; };
-struct F16 { using S = uint16_t; };
-struct F32 { using S = float; };
-
-template <typename D> __device__ __forceinline__ float to_f32(typename D::S x);
-template <> __device__ __forceinline__ float to_f32<BF16>(uint16_t x) {
-  return __uint_as_float(static_cast<uint32_t>(x) << 16);
-}
-template <> __device__ __forceinline__ float to_f32<F16>(uint16_t x) {
-  _Float16 h;
-  __builtin_memcpy(&h, &x, 2);
-  return static_cast<float>(h);
-}
-template <> __device__ __forceinline__ float to_f32<F32>(float x) { return x; }
-
-template <typename D> __device__ __forceinline__ typename D::S from_f32(float x);
-template <> __device__ __forceinline__ uint16_t from_f32<BF16>(float x) {
-  // Round to nearest even on the upper 16 bits; quiet NaNs stay NaN.
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-template <> __device__ __forceinline__ uint16_t from_f32<F16>(float x) {
-  _Float16 h = static_cast<_Float16>(x);
-  uint16_t r;
-  __builtin_memcpy(&r, &h, 2);
-  return r;
-}
-template <> __device__ __forceinline__ float from_f32<F32>(float x) { return x; }
 
 template <typename KD, typename CD, bool NEOX, int VP>
 __global__ void __launch_bounds__(256)
@@ -116,17 +81,7 @@ __global__ void __launch_bounds__(256)
     }
   }
   float z1[VP], z2[VP];
-#pragma unroll
-  for (int v = 0; v < VP; ++v) {
-    const float c0 = to_f32<CD>(co.v[v]), s0 = to_f32<CD>(so.v[v]);
-    const float c1 = to_f32<CD>(cn.v[v]), s1 = to_f32<CD>(sn.v[v]);
-    // R(old)^-1: rotation by -angle.
-    const float y1 = x1[v] * c0 + x2[v] * s0;
-    const float y2 = x2[v] * c0 - x1[v] * s0;
-    // R(new).
-    z1[v] = y1 * c1 - y2 * s1;
-    z2[v] = y2 * c1 + y1 * s1;
-  }
+  rerotate<CD, VP>(x1, x2, co, so, cn, sn, z1, z2);
   if constexpr (NEOX) {
     Pack<KS, VP> a, b;
 #pragma unroll

@@ -58,6 +58,8 @@ SIGNATURES = {
     ],
     "lmc_fused_multi_layer_kv_transfer": [_T, _T, _T, _T, _i32, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _vp],
     "lmc_fused_multi_layer_kv_transfer_noalloc": [_T, _T, _T, _i32, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _vp],
+    "lmc_blend_layer_to_paged": [_T, _i32, ctypes.POINTER(_i64), _T, _i32, _T, _T, _T, _T, _i64, _i32, _i32, _i32,
+                                 _vp],
     "lmc_single_layer_kv_transfer": [_T, _T, _i32, _T, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp],
     "lmc_load_and_reshape_flash": [_T, _T, _T, _T, _i32, _vp],
     "lmc_reshape_and_cache_back_flash": [_T, _T, _T, _T, _i32, _vp],

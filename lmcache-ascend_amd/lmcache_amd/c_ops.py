@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import ctypes
 from enum import IntEnum
-from typing import Sequence
+from typing import Optional, Sequence
 
 import torch
 
@@ -400,6 +400,81 @@ def decode_fast_prefsum(cdf, bytestreams, lengths, output) -> None:
 # ---------------------------------------------------------------------------
 # Fused K re-rotation
 # ---------------------------------------------------------------------------
+
+
+def blend_layer_to_paged(
+    memory_objs: Sequence[torch.Tensor],
+    token_starts: Sequence[int],
+    vllm_kv_caches,
+    slot_mapping: torch.Tensor,
+    old_positions: Optional[torch.Tensor] = None,
+    new_positions: Optional[torch.Tensor] = None,
+    cos_sin_cache: Optional[torch.Tensor] = None,
+    head_size: int = 0,
+    is_neox: bool = True,
+    kvcache_format_raw: int = 2,
+    vllm_two_major: bool = False,
+) -> None:
+    """One layer of the CacheBlend connector's retrieve
+    (lmcache_ascend/v1/npu_connector/npu_connectors.py:556-689) in one
+    kernel, with no device buffer.  The paged caches end as after
+
+        buf = zeros([2, N, W]); buf[:, s:s + n_i] = memory_objs[i]
+        rotary_embedding_k_fused(old_positions, new_positions, buf[0], ...)
+        single_layer_kv_transfer(buf, vllm_kv_caches, slot_mapping, False,
+                                 kvcache_format_raw, False, vllm_two_major)
+
+    with N = slot_mapping.numel(), the objects KV_2TD [2, n_i, W] (device or
+    pinned host tensors, not overlapping), and no re-rotation when the
+    positions are None.  Shapes the kernel does not take (keys other than
+    bf16/fp16, rows or heads not in 16-byte pieces, rotary halves not a
+    multiple of 8 dims) run that same sequence with this library's ops."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    objs = list(memory_objs)
+    if len(objs) != len(token_starts):
+        raise ValueError("memory_objs and token_starts differ in length")
+    dev = _device_index(*(caches + [slot_mapping]))
+    carr = (_lib.LmcTensor * max(len(caches), 1))()
+    for i, c in enumerate(caches):
+        carr[i] = _desc(c)
+    oarr = (_lib.LmcTensor * max(len(objs), 1))()
+    for i, o in enumerate(objs):
+        oarr[i] = _desc(o)
+    starts = (ctypes.c_int64 * max(len(objs), 1))(*[int(x) for x in token_starts])
+    s = _desc(slot_mapping)
+    rope = old_positions is not None or new_positions is not None
+    if rope and (old_positions is None or new_positions is None or cos_sin_cache is None):
+        raise ValueError("old_positions, new_positions and cos_sin_cache go together")
+    a = _desc(old_positions) if rope else None
+    b = _desc(new_positions) if rope else None
+    c = _desc(cos_sin_cache) if rope else None
+    status = _L.lmc_blend_layer_to_paged(
+        oarr, len(objs), starts, carr, len(caches), _ref(s),
+        _ref(a) if rope else None, _ref(b) if rope else None, _ref(c) if rope else None,
+        int(head_size), int(bool(is_neox)), int(kvcache_format_raw), int(bool(vllm_two_major)), _stream(dev),
+    )
+    if status != _lib.ERR_NOT_IMPLEMENTED:
+        _run(status)
+        return
+    # The connector's own sequence (npu_connectors.py:597-680), on device.
+    k0 = caches[0]
+    width = k0.shape[-2] * k0.shape[-1]
+    n_tok = int(slot_mapping.numel())
+    buf = torch.zeros((2, n_tok, width), dtype=k0.dtype, device=slot_mapping.device)
+    for o, st in zip(objs, token_starts):
+        buf[:, int(st):int(st) + o.shape[1]].copy_(o, non_blocking=True)
+    if rope:
+        rotary_embedding_k_fused(old_positions, new_positions, buf[0], head_size, cos_sin_cache, is_neox)
+        # Rows no object covers are zeroed after the re-rotation, as the
+        # connector does (npu_connectors.py:647-649).
+        cursor = 0
+        for o, st in sorted(zip(objs, token_starts), key=lambda x: int(x[1])):
+            if int(st) > cursor:
+                buf[:, cursor:int(st)] = 0
+            cursor = max(cursor, int(st) + o.shape[1])
+        if cursor < n_tok:
+            buf[:, cursor:] = 0
+    single_layer_kv_transfer(buf, vllm_kv_caches, slot_mapping, False, kvcache_format_raw, False, vllm_two_major)
 
 
 def rotary_embedding_k_fused(oldPositions, newPositions, key, headSize, cosSinCache, isNeox) -> None:
