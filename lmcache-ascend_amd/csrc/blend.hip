@@ -99,7 +99,7 @@ __device__ __forceinline__ int64_t idx_at(const void *p, int is32, int64_t i) {
 }
 
 template <typename KD, typename CD, bool NEOX, bool ROPE>
-__global__ void __launch_bounds__(kBlendThreads) blend_layer_kernel(const BlendJob job) {
+__global__ void __launch_bounds__(kBlendThreads) blend_layer_rows(const BlendJob job) {
   using V = u32x4;
   using KS = typename KD::S;
   using CS = typename CD::S;
@@ -334,7 +334,7 @@ void launch_groups(const BlendJob &job, dim3 grid, hipStream_t s) {
 
 template <typename KD, typename CD, bool NEOX, bool ROPE>
 void launch_blend(const BlendJob &job, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((blend_layer_kernel<KD, CD, NEOX, ROPE>), grid, dim3(kBlendThreads), 0, s, job);
+  hipLaunchKernelGGL((blend_layer_rows<KD, CD, NEOX, ROPE>), grid, dim3(kBlendThreads), 0, s, job);
 }
 
 template <typename KD>
