@@ -62,14 +62,19 @@ typedef __attribute__((address_space(1))) u32x4 GlobalU32x4;
 #define LMC_KV_WT_STORES 1        // device-scope write-through 16-byte stores
 #endif
 
-// Stores of HBM-only copies.  A 16-byte store is issued at device (agent)
-// scope, which writes through the XCD's L2 instead of leaving the line dirty
-// there: the kernel's end-of-launch L2 write-back then has nothing left to
-// flush, which shortens every launch (MI355X, one 256-token Llama-3-8B chunk
-// per launch: 14.4 -> 13.3 us for a 64 MiB read + write copy).  Narrower
-// vectors keep the streaming hint.
-template <typename T, bool NT> __device__ __forceinline__ void st(T *p, T v) {
-  if constexpr (NT && LMC_KV_WT_STORES && sizeof(T) == 16)
+// Stores of HBM-only copies.  With WT a 16-byte store is issued at device
+// (agent) scope, which writes through the XCD's L2 instead of leaving the
+// line dirty there, so the kernel's end-of-launch L2 write-back has nothing
+// left to flush; without it (and for narrower vectors) the store carries the
+// streaming hint.  Which is faster depends on the kernel (MI355X, three
+// interleaved runs each): the row kernels are faster with streaming stores
+// (8B shape, 16 objects in one launch 0.172 -> 0.170 ms per direction; 32
+// per-layer flash stores 0.259 -> 0.244 ms; Qwen3-32B shape, 128 objects
+// stored in one launch 2.82 -> 2.70 ms), the tile kernel's stores to
+// memory objects are faster written through (MLA-576 store 0.388 -> 0.402
+// ms with streaming stores), and the direct kernels measure the same.
+template <typename T, bool NT, bool WT = true> __device__ __forceinline__ void st(T *p, T v) {
+  if constexpr (NT && WT && LMC_KV_WT_STORES && sizeof(T) == 16)
     __builtin_amdgcn_global_store_b128((GlobalU32x4 *)(p),
                                        __builtin_bit_cast(u32x4, v), "agent");
   else if constexpr (NT && LMC_KV_NT_STORES)

@@ -218,7 +218,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
       for (int s = 0; s < kSegs; ++s) {
         const int64_t o = off0[r] + (s * 64 + lane) * VEC;
-        if (o < nb[r]) st<V, NT>(reinterpret_cast<V *>(dst[r] + o), v[r][s]);
+        if (o < nb[r]) st<V, NT, false>(reinterpret_cast<V *>(dst[r] + o), v[r][s]);
       }
   }
 }
@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(kThreads)
     if (live[r])
 #pragma unroll
       for (int s = 0; s < kSegs; ++s)
-        st<V, NT>(reinterpret_cast<V *>(dst[r] + (s * 64 + lane) * 16), v[r][s]);
+        st<V, NT, false>(reinterpret_cast<V *>(dst[r] + (s * 64 + lane) * 16), v[r][s]);
 }
 
 // Tile kernel.  A wave owns a tile of up to 64 consecutive tokens of one
@@ -372,7 +372,7 @@ __device__ __forceinline__ uint64_t shfl64(uint64_t x, int src_lane) {
          static_cast<uint32_t>(lo);
 }
 
-template <int VEC, bool NT, int NC>
+template <int VEC, bool NT, int NC, bool WT>
 __global__ void __launch_bounds__(kThreads)
     kv_tiles_copy(const CopyJob job, const ChunkListT<NC> chunks, int tile_rows) {
   using V = typename VecOf<VEC>::T;
@@ -462,7 +462,7 @@ __global__ void __launch_bounds__(kThreads)
       }
 #pragma unroll
       for (int u = 0; u < kTileU; ++u)
-        if (live[u]) st<V, NT>(reinterpret_cast<V *>(dst[u]), v[u]);
+        if (live[u]) st<V, NT, WT>(reinterpret_cast<V *>(dst[u]), v[u]);
     }
   }
 }
@@ -637,16 +637,26 @@ void launch_vec(const CopyJob &job_in, const ChunkList &chunks, int n_chunks,
           "too many tiles in one chunk");
     int gx = static_cast<int>((tiles + kWaves - 1) / kWaves);
     dim3 grid(std::max(1, std::min(gx, LMC_KV_GRID_CAP)), n_chunks);
+    // Stores into memory objects are written through, stores into the paged
+    // caches stream (see st()).
+    const bool wt = job.page2lmc != 0;
     if (n_chunks == 1) {
       const ChunkListT<1> one = first_chunk(chunks);
-      if (nt)
-        hipLaunchKernelGGL((kv_tiles_copy<VEC, true, 1>), grid, block, 0, stream, job, one, tile_rows);
+      if (nt && wt)
+        hipLaunchKernelGGL((kv_tiles_copy<VEC, true, 1, true>), grid, block, 0, stream, job, one, tile_rows);
+      else if (nt)
+        hipLaunchKernelGGL((kv_tiles_copy<VEC, true, 1, false>), grid, block, 0, stream, job, one, tile_rows);
       else
-        hipLaunchKernelGGL((kv_tiles_copy<VEC, false, 1>), grid, block, 0, stream, job, one, tile_rows);
+        hipLaunchKernelGGL((kv_tiles_copy<VEC, false, 1, false>), grid, block, 0, stream, job, one, tile_rows);
+    } else if (nt && wt) {
+      hipLaunchKernelGGL((kv_tiles_copy<VEC, true, kMaxChunks, true>), grid, block, 0, stream, job, chunks,
+                         tile_rows);
     } else if (nt) {
-      hipLaunchKernelGGL((kv_tiles_copy<VEC, true, kMaxChunks>), grid, block, 0, stream, job, chunks, tile_rows);
+      hipLaunchKernelGGL((kv_tiles_copy<VEC, true, kMaxChunks, false>), grid, block, 0, stream, job, chunks,
+                         tile_rows);
     } else {
-      hipLaunchKernelGGL((kv_tiles_copy<VEC, false, kMaxChunks>), grid, block, 0, stream, job, chunks, tile_rows);
+      hipLaunchKernelGGL((kv_tiles_copy<VEC, false, kMaxChunks, false>), grid, block, 0, stream, job, chunks,
+                         tile_rows);
     }
   }
 }
