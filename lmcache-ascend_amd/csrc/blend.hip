@@ -16,12 +16,19 @@
 //
 // Work mapping: a segment is one memory object or one run of uncovered
 // tokens; grid.y enumerates the segments of a launch, grid.x the segment's
-// rows, one wave per (token, plane) row with the K and V rows of a token in
-// adjacent waves.  K rows with in-range positions: lane work is a group of
-// eight rotation pairs (two 16-byte halves for neox, one 32-byte run for
-// GPT-J), head_size - rot pass-through dims per head as 16-byte pieces.
-// Every other row moves as 16-byte pieces.  Slots outside [0, num_slots)
-// are skipped, as in the single-layer transfer.
+// tokens.  Two kernels:
+//  - blend_layer_groups, for rows without re-rotation and for heads of 256
+//    bytes rotated whole (the common bf16/fp16 x 128 case): a 16-lane group
+//    per token moves its K row (re-rotated: neox partners sit 8 lanes apart
+//    and are exchanged with one DPP rotation, GPT-J pairs are adjacent dims
+//    of one lane), then its V row, one 16-byte access per lane in flight.
+//  - blend_layer_rows, for the other head shapes: one wave per (token,
+//    plane) row with the K and V rows of a token in adjacent waves; on K
+//    rows with in-range positions lane work is a group of eight rotation
+//    pairs (two 16-byte halves for neox, one 32-byte run for GPT-J), and
+//    head_size - rot pass-through dims per head move as 16-byte pieces.
+// Slots outside [0, num_slots) are skipped, as in the single-layer
+// transfer.
 #include "kv_geom.h"
 #include "rope_math.h"
 
@@ -386,6 +393,7 @@ extern "C" int lmc_blend_layer_to_paged(const lmc_tensor *objects, int32_t n_obj
     const LayerGeom g = layer_geom(caches, n_caches, kvcache_format, vllm_two_major != 0, 0, 0, 0);
     check(g.n_planes == 2, "blend_layer_to_paged: caches must have a K and a V plane");
     const lmc_tensor &slots = slots_of(slot_mapping);
+    check(slots.device < 0 || slots.device == g.device, "slot_mapping must be on the caches' device");
     const int64_t N = slots.sizes[0];
     const int64_t W = g.width[0];
     const int64_t es = g.es;
@@ -423,8 +431,11 @@ extern "C" int lmc_blend_layer_to_paged(const lmc_tensor *objects, int32_t n_obj
       check((t.sizes[1] <= 1 || t.strides[1] == W) && (W <= 1 || t.strides[2] == 1) &&
                 (t.sizes[1] == 0 || t.strides[0] == t.sizes[1] * W),
             "memory objects must be contiguous");
+      check(t.device < 0 || t.device == g.device,
+            "memory objects must be in pinned host memory or on the caches' device");
       const int64_t n = t.sizes[1];
       const int64_t s0 = so.first;
+      check(s0 >= 0, "token_starts must be non-negative");
       check(s0 >= cursor, "memory objects must not overlap");
       check(s0 + n <= N, "memory object token range exceeds slot_mapping");
       if (s0 > cursor) segs.push_back({0, cursor, s0 - cursor, 0});
@@ -459,7 +470,8 @@ extern "C" int lmc_blend_layer_to_paged(const lmc_tensor *objects, int32_t n_obj
       check(op.dtype == np_.dtype && (op.dtype == LMC_I64 || op.dtype == LMC_I32),
             "positions must both be int64 or int32");
       check((N <= 1 || (op.strides[0] == 1 && np_.strides[0] == 1)), "positions must be contiguous");
-      check(op.device >= 0 && np_.device >= 0 && c.device >= 0, "positions and cos_sin_cache must be device tensors");
+      check(op.device == g.device && np_.device == g.device && c.device == g.device,
+            "positions and cos_sin_cache must be on the caches' device");
       check(c.ndim >= 1, "cos_sin_cache must have a last dimension");
       const int64_t rot = size(c, -1);
       check(head_size > 0 && W % head_size == 0, "key width is not a multiple of head_size");

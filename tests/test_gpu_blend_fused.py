@@ -78,7 +78,7 @@ def _expected(caches, fmt, two_major, objs, starts, n_tok, slots, rope):
     return want
 
 
-def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout, seed):
+def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout, seed, slot_dtype=torch.int64):
     gen = torch.Generator().manual_seed(seed)
     caches = _caches(fmt, two_major, dtype, gen)
     gpu = caches.to(DEV) if isinstance(caches, torch.Tensor) else tuple(c.to(DEV) for c in caches)
@@ -113,7 +113,8 @@ def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout,
         kwargs = dict(old_positions=old.to(pdt).to(DEV), new_positions=new.to(pdt).to(DEV),
                       cos_sin_cache=cache.to(DEV), head_size=D, is_neox=neox)
     want = _expected(caches, fmt, two_major, objs, starts, n_tok, slots, rope)
-    ops.blend_layer_to_paged(dobjs, starts, gpu, slots.to(DEV), kvcache_format_raw=fmt, vllm_two_major=two_major,
+    ops.blend_layer_to_paged(dobjs, starts, gpu, slots.to(slot_dtype).to(DEV), kvcache_format_raw=fmt,
+                             vllm_two_major=two_major,
                              **kwargs)
     torch.cuda.synchronize()
     got = (gpu,) if isinstance(gpu, torch.Tensor) else gpu
@@ -168,3 +169,63 @@ def test_blend_layer_rejects_overlapping_objects(ops):
         ops.blend_layer_to_paged(objs, [0, 5], gpu, slots, kvcache_format_raw=2)
     with pytest.raises(RuntimeError, match="exceeds slot_mapping"):
         ops.blend_layer_to_paged(objs[:1], [25], gpu, slots, kvcache_format_raw=2)
+
+
+def test_blend_layer_int32_slots(ops):
+    _run_case(ops, 2, False, torch.bfloat16, "pinned", "i64", True, D, "gaps", seed=31, slot_dtype=torch.int32)
+
+
+def test_blend_layer_rejects_host_positions(ops):
+    gen = torch.Generator().manual_seed(37)
+    gpu = tuple(c.to(DEV) for c in _caches(2, False, torch.bfloat16, gen))
+    objs = [torch.zeros((2, 10, W), dtype=torch.bfloat16, device=DEV)]
+    slots = torch.arange(10, dtype=torch.int64, device=DEV)
+    cache = orope.cos_sin_cache(64, D, 10000.0).to(torch.bfloat16).to(DEV)
+    pos = torch.arange(10, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="on the caches' device"):
+        ops.blend_layer_to_paged(objs, [0], gpu, slots, old_positions=pos, new_positions=pos.to(DEV),
+                                 cos_sin_cache=cache, head_size=D, kvcache_format_raw=2)
+    with pytest.raises(RuntimeError, match="non-negative"):
+        ops.blend_layer_to_paged(objs, [-1], gpu, slots, kvcache_format_raw=2)
+
+
+def test_blend_layer_graph_replays(ops):
+    """Captured once in a HIP graph; each replay reads the objects' current
+    contents and positions (refilled by eager copies between replays) and
+    must equal the oracle's connector sequence on them."""
+    gen = torch.Generator().manual_seed(41)
+    caches = _caches(2, False, torch.bfloat16, gen)
+    gpu = tuple(c.to(DEV) for c in caches)
+    sizes, starts = [64, 100], [0, 70]
+    n_tok = 180
+    objs = [torch.randn((2, n, W), generator=gen).to(torch.bfloat16).pin_memory() for n in sizes]
+    slots = torch.tensor(sample_slots(NB * BS, n_tok, seed=41), dtype=torch.int64)
+    max_pos = 2048
+    cache = orope.cos_sin_cache(max_pos, D, 500000.0).to(torch.bfloat16)
+    old = torch.zeros(n_tok, dtype=torch.int64, device=DEV)
+    new = torch.zeros(n_tok, dtype=torch.int64, device=DEV)
+    dslots, dcache = slots.to(DEV), cache.to(DEV)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        ops.blend_layer_to_paged(objs, starts, gpu, dslots, old_positions=old, new_positions=new,
+                                 cos_sin_cache=dcache, head_size=D, is_neox=True, kvcache_format_raw=2)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.blend_layer_to_paged(objs, starts, gpu, dslots, old_positions=old, new_positions=new,
+                                 cos_sin_cache=dcache, head_size=D, is_neox=True, kvcache_format_raw=2)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in objs:
+            o.copy_(torch.randn(o.shape, generator=gen).to(torch.bfloat16))
+        o_pos = torch.randint(0, max_pos - 600, (n_tok,), generator=gen)
+        n_pos = o_pos + 100 * (rep + 1)
+        old.copy_(o_pos)
+        new.copy_(n_pos)
+        torch.cuda.synchronize()
+        want = _expected(tuple(c.cpu() for c in gpu), 2, False, objs, starts, n_tok, slots,
+                         (o_pos, n_pos, cache, D, True))
+        graph.replay()
+        torch.cuda.synchronize()
+        for g, w in zip(gpu, want):
+            assert np.array_equal(to_bytes(g), w.data), f"replay {rep}"
