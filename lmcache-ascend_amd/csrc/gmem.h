@@ -12,3 +12,12 @@ template <typename T> __device__ __forceinline__ T gload(const T *p) {
 template <typename T> __device__ __forceinline__ void gstore(T *p, T v) {
   *reinterpret_cast<__attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p)) = v;
 }
+
+// The same with the streaming (non-temporal) hint.
+template <typename T> __device__ __forceinline__ T gload_nt(const T *p) {
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const __attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p)));
+}
+template <typename T> __device__ __forceinline__ void gstore_nt(T *p, T v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<__attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p)));
+}

@@ -81,7 +81,19 @@ __device__ __forceinline__ int64_t c8_index(const void *p, int is32, int64_t i) 
 // 64 / kC8Group x kC8Unroll consecutive tokens.  Each lane issues every key load of the group's tokens (one or two 16-byte
 // accesses per token for 128- or 256-byte keys), then the stores; lane u of
 // the group moves token u's 2-byte scale.
-template <int kC8Group, int kC8Unroll>
+// Key rows are stored with the streaming hint when the destination is the
+// cache (unpacking), which is always device memory; packing writes packets
+// that may be page-locked host memory (the packet table holds device
+// values, so the host cannot tell), and stores there keep the plain form.
+// Measured on MI355X (8 layers x 16384 tokens, three runs each): unpack
+// from device packets 0.0124 -> 0.0110 ms, from pinned packets unchanged
+// (0.307 ms); streaming stores into device packets 0.0106 -> 0.0094 ms but
+// into pinned packets 0.312 -> 0.362 ms.
+template <bool kNtStores, typename T> __device__ __forceinline__ void c8_st(T *p, T v) {
+  if constexpr (kNtStores) gstore_nt(p, v); else gstore(p, v);
+}
+
+template <int kC8Group, int kC8Unroll, bool kNtStores>
 __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   using V = unsigned int __attribute__((ext_vector_type(4)));
   constexpr int kKeyVecs = 256 / 16 / kC8Group;  // per lane, widest key row
@@ -156,7 +168,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
       V *dst = reinterpret_cast<V *>(job.from_npu ? packet + tok(u) * kb : L.keys + phys[u] * kb);
 #pragma unroll
       for (int k = 0; k < kKeyVecs; ++k)
-        if (gl + k * kC8Group < nv) gstore(dst + gl + k * kC8Group, x[u][k]);
+        if (gl + k * kC8Group < nv) c8_st<kNtStores>(dst + gl + k * kC8Group, x[u][k]);
     }
   } else {
 #pragma unroll
@@ -312,9 +324,10 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks), nl);
     if (from_npu)
-      hipLaunchKernelGGL((indexer_c8_copy<kPackGroup, kPackUnroll>), grid, dim3(kC8Threads), 0, stream, j);
+      hipLaunchKernelGGL((indexer_c8_copy<kPackGroup, kPackUnroll, false>), grid, dim3(kC8Threads), 0, stream,
+                         j);
     else
-      hipLaunchKernelGGL((indexer_c8_copy<kUnpackGroup, kUnpackUnroll>), grid, dim3(kC8Threads), 0, stream,
+      hipLaunchKernelGGL((indexer_c8_copy<kUnpackGroup, kUnpackUnroll, true>), grid, dim3(kC8Threads), 0, stream,
                          j);
     hip_check(hipGetLastError(), "indexer_c8_copy launch");
   }

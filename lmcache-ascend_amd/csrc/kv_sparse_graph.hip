@@ -30,6 +30,12 @@ namespace {
 
 constexpr int kSfaThreads = 256;
 constexpr int kSfaUnroll = 4;  // 16-byte accesses per lane and row in one pass
+// Rows are stored with the streaming hint: the destinations are always the
+// device caches, and the copy leaves nothing another kernel reads soon.
+// Measured on MI355X (64 requests x 2048 selected MLA rows, three runs
+// each): device sources 0.0684-0.0687 -> 0.0530-0.0532 ms, pinned host
+// sources unchanged (2.764 ms); streaming loads as well gave 0.0675-0.0678
+// ms from device sources, so loads stay plain.
 
 struct SfaJob {
   uint64_t k;
@@ -59,7 +65,7 @@ __device__ __forceinline__ void sfa_row(uint8_t *dst, const uint8_t *src,
                                         int bytes, int gl, int G) {
   if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
     for (int v = gl; v < bytes / 16; v += G)
-      gstore(reinterpret_cast<SfaVec *>(dst) + v, gload(reinterpret_cast<const SfaVec *>(src) + v));
+      gstore_nt(reinterpret_cast<SfaVec *>(dst) + v, gload(reinterpret_cast<const SfaVec *>(src) + v));
   } else {
     for (int b = gl; b < bytes; b += G) dst[b] = src[b];
   }
@@ -111,8 +117,8 @@ __global__ void __launch_bounds__(kSfaThreads) sfa_copy(SfaJob job) {
 #pragma unroll
     for (int u = 0; u < kSfaUnroll; ++u) {
       const int v = gl + u * G;
-      if (v < kv) gstore(reinterpret_cast<SfaVec *>(kdst) + v, xk[u]);
-      if (v < pv) gstore(reinterpret_cast<SfaVec *>(pdst) + v, xp[u]);
+      if (v < kv) gstore_nt(reinterpret_cast<SfaVec *>(kdst) + v, xk[u]);
+      if (v < pv) gstore_nt(reinterpret_cast<SfaVec *>(pdst) + v, xp[u]);
     }
     return;
   }
