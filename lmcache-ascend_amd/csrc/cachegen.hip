@@ -31,6 +31,14 @@
 #include <type_traits>
 #include "common.h"
 #include "cachegen_decode.h"
+#include "gmem.h"
+
+// Output words (CDF rows, bitstream words, decoded symbols) are stored with
+// the streaming hint: nothing in the kernel reads them back.  Measured on
+// MI355X (32 layers x 256 tokens x 1024 channels, K and V, three runs each,
+// event times): decode 27.3-27.5 -> 25.2-25.3 us, encode 19.9-20.0 ->
+// 19.2-19.5 us.
+template <typename T> __device__ __forceinline__ void cg_st(T *p, T v) { gstore_nt(p, v); }
 
 namespace lmc {
 
@@ -353,7 +361,7 @@ __global__ void __launch_bounds__(kCdfThreads)
   const int total = cnt * (nb + 1);
   if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
     for (int i = tid; i < total / 2; i += kCdfThreads)
-      reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(rows)[i];
+      cg_st(reinterpret_cast<uint32_t *>(dst) + i, reinterpret_cast<const uint32_t *>(rows)[i]);
     if ((total & 1) && tid == 0) dst[total - 1] = rows[total - 1];
   } else {
     for (int i = tid; i < total; i += kCdfThreads) dst[i] = rows[i];
@@ -422,7 +430,7 @@ __global__ void __launch_bounds__(kEncLanes)
       if (nbits >= 32) {
         const uint32_t word = static_cast<uint32_t>(acc >> (nbits - 32));
         if (word_stores && wpos + 4 <= chunk)
-          *reinterpret_cast<uint32_t *>(row + wpos) = __builtin_bswap32(word);
+          cg_st(reinterpret_cast<uint32_t *>(row + wpos), __builtin_bswap32(word));
         else
           put_bytes(row, chunk, wpos, word, 4);
         wpos += 4;
@@ -468,7 +476,7 @@ __device__ __forceinline__ void put_word(uint8_t *row, int64_t chunk, uint32_t i
                                          int n, int word_stores) {
   const int64_t at = static_cast<int64_t>(idx) * 4;
   if (n == 4 && word_stores && at + 4 <= chunk)
-    *reinterpret_cast<uint32_t *>(row + at) = __builtin_bswap32(word);
+    cg_st(reinterpret_cast<uint32_t *>(row + at), __builtin_bswap32(word));
   else
     put_bytes(row, chunk, at, word, n);
 }
@@ -877,7 +885,7 @@ __global__ void __launch_bounds__(64 * PIECES)
     const uint32_t *brow = bits + st * row_words;
     const uint32_t nw = word_stores ? nbytes >> 2 : 0u;
     for (uint32_t k = lane; k < nw; k += kEncLanes)
-      reinterpret_cast<uint32_t *>(orow)[k] = __builtin_bswap32(brow[k]);
+      cg_st(reinterpret_cast<uint32_t *>(orow) + k, __builtin_bswap32(brow[k]));
     for (uint32_t b = 4 * nw + lane; b < nbytes; b += kEncLanes)
       orow[b] = static_cast<uint8_t>(brow[b >> 2] >> (24 - 8 * (b & 3u)));
   }
@@ -1148,14 +1156,14 @@ __device__ __forceinline__ void decode_block_fast(const Tab &tb, int T, int C,
 #pragma unroll
     for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
     wave_sync();
-    *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
     odst += step4;
     wave_sync();
   }
   if (t < T) {
     for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
     wave_sync();
-    if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    if ((lane >> 4) < T - t) cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
   }
 }
 
@@ -1180,14 +1188,14 @@ __device__ __forceinline__ void decode_block_bytes(const cgdec::ByteTables &tb, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
     wave_sync();
-    *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
     odst += step4;
     wave_sync();
   }
   if (t < T) {
     for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(step());
     wave_sync();
-    if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+    if ((lane >> 4) < T - t) cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
   }
 }
 
@@ -1470,7 +1478,7 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
       cur.refill();
       __builtin_amdgcn_sched_barrier(0);
       if (t > 0) {
-        *odst = (word >> 3) & 0x1F1F1F1Fu;
+        cg_st(odst, (word >> 3) & 0x1F1F1F1Fu);
         odst += step4;
       }
       obuf[lane] = static_cast<uint8_t>(e0);
@@ -1482,7 +1490,7 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
       wave_sync();
     }
     if (t > 0) {
-      *odst = (word >> 3) & 0x1F1F1F1Fu;
+      cg_st(odst, (word >> 3) & 0x1F1F1F1Fu);
       odst += step4;
     }
     if (t < T) {
@@ -1491,7 +1499,7 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
         if (i & 1) cur.refill();
       }
       wave_sync();
-      if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      if ((lane >> 4) < T - t) cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
     }
   } else {
     tb.finish();
@@ -1507,14 +1515,14 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
 #pragma unroll
       for (int i = 0; i < 4; ++i) obuf[i * kDecLanes + lane] = step();
       wave_sync();
-      *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
       odst += step4;
       wave_sync();
     }
     if (t < T) {
       for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = step();
       wave_sync();
-      if ((lane >> 4) < T - t) *odst = reinterpret_cast<const uint32_t *>(obuf)[lane];
+      if ((lane >> 4) < T - t) cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
     }
   }
   return true;
