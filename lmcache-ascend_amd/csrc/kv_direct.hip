@@ -232,7 +232,7 @@ __device__ __forceinline__ void copy_entry(const EntryJob &job, int64_t e, int g
       for (int k = 0; k < kEntUnroll; ++k) {
         const int v = gl + k * G;
         if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes)
-          x[p][k] = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + v);
+          x[p][k] = gload(reinterpret_cast<const V *>(src[p]) + v);
       }
 #pragma unroll
     for (int p = 0; p < kMaxPlanes; ++p)
@@ -251,7 +251,7 @@ __device__ __forceinline__ void copy_entry(const EntryJob &job, int64_t e, int g
     if (p >= job.n_planes) continue;
     const int64_t nv = job.plane[p].row_bytes / VEC;
     for (int64_t v = gl; v < nv; v += G) {
-      const V x = ld<V, NT>(reinterpret_cast<const V *>(src[p]) + v);
+      const V x = gload(reinterpret_cast<const V *>(src[p]) + v);
       st<V, NT>(reinterpret_cast<V *>(dst[p]) + v, x);
       if (third) st<V, NT>(reinterpret_cast<V *>(mir[p]) + v, x);
     }
@@ -278,6 +278,10 @@ __global__ void __launch_bounds__(kEntThreads) kv_entry_copy(EntryJob job) {
 // and copy_entry().  Measured on MI355X, 65536 MLA tokens (1024 + 128-byte
 // rows) scattered from a device buffer: 29.6 us against 30.7 us with one
 // entry per group.
+// Row loads of these kernels are plain (no streaming hint): their rows are
+// gathered at random, and the same scatter took 31.6-32.1 us (events)
+// with streaming loads against 27.8-28.0 us without; the host-memory
+// paths measure the same either way.  Stores keep st().
 template <int VEC, bool NT>
 __global__ void __launch_bounds__(kEntThreads) kv_entry_pair_copy(EntryJob job) {
   using V = typename VecOf<VEC>::T;
@@ -344,7 +348,7 @@ __global__ void __launch_bounds__(kEntThreads) kv_entry_pair_copy(EntryJob job) 
       for (int u = 0; u < kEntUnroll; ++u) {
         const int v = gl + u * G;
         if (p < job.n_planes && static_cast<int64_t>(v) * VEC < job.plane[p].row_bytes)
-          x[k][p][u] = ld<V, NT>(reinterpret_cast<const V *>(src[k][p]) + v);
+          x[k][p][u] = gload(reinterpret_cast<const V *>(src[k][p]) + v);
       }
   }
 #pragma unroll
