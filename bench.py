@@ -383,6 +383,20 @@ def bench_blend(torch, ops, dev, stream, flat, slots):
     t_fused_one = time_events(torch, stream, lambda: ops.blend_layer_to_paged(
         objs[0], obj_starts, (flat[0], flat[1]), slots, old_positions=old, new_positions=new, cos_sin_cache=cache,
         head_size=D, is_neox=True, kvcache_format_raw=2), 20)[0]
+    # The same calls with the memory objects in device memory (an HBM-bound
+    # layer load: 2 x 16 MiB of traffic per layer), each layer its own objects.
+    dhost = host.to(dev)
+    dobjs = [[dhost[layer, c] for c in range(n_obj)] for layer in range(L)]
+
+    def fused_layers_device():
+        for layer in range(L):
+            ops.blend_layer_to_paged(dobjs[layer], obj_starts, (flat[2 * layer], flat[2 * layer + 1]), slots,
+                                     old_positions=old, new_positions=new, cos_sin_cache=cache, head_size=D,
+                                     is_neox=True, kvcache_format_raw=2)
+
+    fused_layers_device()
+    t_fused_dev = time_events(torch, stream, fused_layers_device, 5)[0]
+    del dhost, dobjs
     with torch.cuda.stream(load_stream):
         t_h2d = time_events(torch, load_stream, lambda: h2d(bufs[0], 0), 10)[0]
     t_rope = time_events(torch, stream, lambda: rope(bufs[1]), 20)[0]
@@ -402,6 +416,10 @@ def bench_blend(torch, ops, dev, stream, flat, slots):
                                              "payload_GBps": round(layer_bytes / (t_fused_one * 1e-3) / 1e9, 2),
                                              "pcie_frac": round(layer_bytes / (t_fused_one * 1e-3) / 1e9 / PCIE_PEAK_GBS,
                                                                 4)}
+    out["blend_layer_to_paged_device_objects_32_layers"] = {
+        "ms": round(t_fused_dev, 4), "ms_per_layer": round(t_fused_dev / L, 4),
+        "hbm_GBps": round(2 * layer_bytes * L / (t_fused_dev * 1e-3) / 1e9, 1),
+        "hbm_frac": round(2 * layer_bytes * L / (t_fused_dev * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     out["blend_stage_scatter_one_layer"] = {"ms": round(t_scatter, 4),
                                             "hbm_GBps": round(2 * layer_bytes / (t_scatter * 1e-3) / 1e9, 1)}
     del host, bufs

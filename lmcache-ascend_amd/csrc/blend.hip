@@ -223,24 +223,37 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_rows(const BlendJob
 // Tokens by 16-lane groups, for rows without re-rotation and for K rows
 // whose heads are 256 bytes with every dim rotated (128 bf16 / fp16 dims:
 // the 16 lanes' 16-byte accesses cover one head).  A group walks the
-// token's K row, then its V row, with one 16-byte access per lane in
-// flight, and the groups stride over the segment's tokens: reads of page-locked host memory move the most bytes
-// over PCIe with few reads in flight (the copy kernels of kv_direct.hip
-// measured the same).  Neox pairs (i, i + 64) sit in lanes q and q ^ 8 of a
-// head: one DPP rotation by 8 within the 16-lane row gives each lane its
-// partner's values, and each lane writes its own half.  GPT-J pairs are
-// adjacent dims, four whole pairs per lane.
-template <typename KD, typename CD, bool NEOX, bool ROPE>
+// token's K row, then its V row, kU 16-byte accesses per lane in flight,
+// and the groups stride over the segment's tokens.  Objects in page-locked
+// host memory take kU = 1: reads over PCIe move the most bytes with few
+// reads in flight (the copy kernels of kv_direct.hip measured the same);
+// objects in device memory take kU = 8 (a 2 KiB row per group in one
+// pass).  Neox pairs (i, i + 64) sit in lanes q and q ^ 8 of a head: one
+// DPP rotation by 8 within the 16-lane row gives each lane its partner's
+// values, and each lane writes its own half.  GPT-J pairs are adjacent
+// dims, four whole pairs per lane.  The cos/sin values a lane needs are the
+// same for every head of the token and are loaded once.
+template <typename KD, typename CD, bool NEOX, bool ROPE, int kU>
 __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJob job) {
   using V = u32x4;
   using KS = typename KD::S;
   using CS = typename CD::S;
   constexpr int kGroups = kBlendThreads / 16;
+  constexpr int kPairs = NEOX ? 8 : 4;  // rotation pairs per lane and head
   const BlendSeg &sg = job.seg[blockIdx.y];
   const int q = threadIdx.x & 15;
   const int64_t rb = job.row_bytes;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kGroups + (threadIdx.x >> 4); i < sg.count;
-       i += static_cast<int64_t>(gridDim.x) * kGroups) {
+  // kU > 1 (device objects): a group owns one (token, plane) row; the four
+  // groups of an even wave take the K rows of four tokens and those of the
+  // next wave the same tokens' V rows, so the re-rotation runs on full
+  // waves.  kU = 1: a group owns a token.
+  constexpr int kRowsPerItem = kU > 1 ? 1 : 2;
+  const int64_t items = kU > 1 ? (sg.count + 3) / 4 * 8 : sg.count;
+  for (int64_t it = static_cast<int64_t>(blockIdx.x) * kGroups + (threadIdx.x >> 4); it < items;
+       it += static_cast<int64_t>(gridDim.x) * kGroups) {
+    const int64_t i = kU > 1 ? ((it >> 2) >> 1) * 4 + (it & 3) : it;
+    const int p0 = kU > 1 ? static_cast<int>((it >> 2) & 1) : 0;
+    if (i >= sg.count) continue;
     const int64_t j = sg.tok0 + i;
     const int64_t slot = idx_at(job.slots, job.slot_i32, j);
     if (slot < 0 || slot >= job.num_slots) continue;
@@ -252,16 +265,31 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
       in_blk = s32 - static_cast<uint32_t>(blk) * bs;
     }
     bool rotate = false;
-    const CS *crow_o = nullptr, *crow_n = nullptr;
-    if constexpr (ROPE) {
+    Pack<CS, kPairs> co{}, so{}, cn{}, sn{};
+    if (ROPE && p0 == 0) {
       const int64_t po = idx_at(job.old_pos, job.pos_i32, j);
       const int64_t pn = idx_at(job.new_pos, job.pos_i32, j);
-      rotate = po >= 0 && po < job.max_pos && pn >= 0 && pn < job.max_pos;
-      crow_o = static_cast<const CS *>(job.cache) + po * job.rot;
-      crow_n = static_cast<const CS *>(job.cache) + pn * job.rot;
+      rotate = sg.src != 0 && po >= 0 && po < job.max_pos && pn >= 0 && pn < job.max_pos;
+      if (rotate) {
+        const CS *crow_o = static_cast<const CS *>(job.cache) + po * job.rot;
+        const CS *crow_n = static_cast<const CS *>(job.cache) + pn * job.rot;
+        const int i0 = NEOX ? (q & 7) * 8 : q * 4;
+        if constexpr (NEOX) {
+          co = load_pack<Pack<CS, 8>>(crow_o + i0);
+          so = load_pack<Pack<CS, 8>>(crow_o + job.rot / 2 + i0);
+          cn = load_pack<Pack<CS, 8>>(crow_n + i0);
+          sn = load_pack<Pack<CS, 8>>(crow_n + job.rot / 2 + i0);
+        } else {
+          co = load_half_pack<CS>(crow_o + i0);
+          so = load_half_pack<CS>(crow_o + job.rot / 2 + i0);
+          cn = load_half_pack<CS>(crow_n + i0);
+          sn = load_half_pack<CS>(crow_n + job.rot / 2 + i0);
+        }
+      }
     }
-    // The token's K row, then its V row.
-    for (int p = 0; p < 2; ++p) {
+    // The item's rows: the token's K row, then its V row (or the one row).
+    for (int r = 0; r < kRowsPerItem; ++r) {
+      const int p = p0 + r;
       const PlaneDesc &pd = job.plane[p];
       uint8_t *dst = reinterpret_cast<uint8_t *>(job.base[p]) + pd.paged_off + blk * pd.blk_stride +
                      in_blk * pd.row_pitch;
@@ -271,63 +299,59 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
         continue;
       }
       const uint8_t *src = reinterpret_cast<const uint8_t *>(sg.src) + p * sg.plane_bytes + i * rb;
-      if (!(ROPE && p == 0 && rotate)) {
-        // One read in flight per lane.
+      const bool rot_row = ROPE && p == 0 && rotate;
 #pragma unroll 1
-        for (int64_t o = static_cast<int64_t>(q) * 16; o < rb; o += 256)
-          gstore(reinterpret_cast<V *>(dst + o), gload(reinterpret_cast<const V *>(src + o)));
-        continue;
-      }
-      if constexpr (ROPE) {
-        // One head per step: lane q holds dims [8q, 8q + 8) of it.
-        for (int64_t o = static_cast<int64_t>(q) * 16; o < rb; o += 256) {
-          const V raw = gload(reinterpret_cast<const V *>(src + o));
-          const Pack<KS, 8> mine = __builtin_bit_cast(Pack<KS, 8>, raw);
-          if constexpr (NEOX) {
-            V other;
+      for (int64_t base = static_cast<int64_t>(q) * 16; base < rb; base += kU * 256) {
+        V raw[kU];
 #pragma unroll
-            for (int w = 0; w < 4; ++w)  // row_ror:8 within the 16-lane row
-              other[w] = static_cast<uint32_t>(
-                  __builtin_amdgcn_update_dpp(0, static_cast<int>(raw[w]), 0x128, 0xF, 0xF, false));
-            const Pack<KS, 8> part = __builtin_bit_cast(Pack<KS, 8>, other);
-            const bool lo = q < 8;
-            const int i0 = (q & 7) * 8;
-            const Pack<CS, 8> co = load_pack<Pack<CS, 8>>(crow_o + i0);
-            const Pack<CS, 8> so = load_pack<Pack<CS, 8>>(crow_o + job.rot / 2 + i0);
-            const Pack<CS, 8> cn = load_pack<Pack<CS, 8>>(crow_n + i0);
-            const Pack<CS, 8> sn = load_pack<Pack<CS, 8>>(crow_n + job.rot / 2 + i0);
-            float x1[8], x2[8], z1[8], z2[8];
+        for (int u = 0; u < kU; ++u)
+          if (base + u * 256 < rb) raw[u] = gload(reinterpret_cast<const V *>(src + base + u * 256));
 #pragma unroll
-            for (int v = 0; v < 8; ++v) {
-              x1[v] = to_f32<KD>(lo ? mine.v[v] : part.v[v]);
-              x2[v] = to_f32<KD>(lo ? part.v[v] : mine.v[v]);
+        for (int u = 0; u < kU; ++u) {
+          const int64_t o = base + u * 256;
+          if (o >= rb) continue;
+          V w = raw[u];
+          if constexpr (ROPE) {
+            // Rows that rotate are whole heads, so `o < rb` holds for all
+            // 16 lanes of the group together (the DPP partner is active).
+            if (rot_row) {
+              const Pack<KS, 8> mine = __builtin_bit_cast(Pack<KS, 8>, w);
+              Pack<KS, 8> out;
+              if constexpr (NEOX) {
+                V other;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)  // row_ror:8 within the 16-lane row
+                  other[k] = static_cast<uint32_t>(
+                      __builtin_amdgcn_update_dpp(0, static_cast<int>(w[k]), 0x128, 0xF, 0xF, false));
+                const Pack<KS, 8> part = __builtin_bit_cast(Pack<KS, 8>, other);
+                const bool lo = q < 8;
+                float x1[8], x2[8], z1[8], z2[8];
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                  x1[v] = to_f32<KD>(lo ? mine.v[v] : part.v[v]);
+                  x2[v] = to_f32<KD>(lo ? part.v[v] : mine.v[v]);
+                }
+                rerotate<CD, 8>(x1, x2, co, so, cn, sn, z1, z2);
+#pragma unroll
+                for (int v = 0; v < 8; ++v) out.v[v] = from_f32<KD>(lo ? z1[v] : z2[v]);
+              } else {
+                float x1[4], x2[4], z1[4], z2[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                  x1[v] = to_f32<KD>(mine.v[2 * v]);
+                  x2[v] = to_f32<KD>(mine.v[2 * v + 1]);
+                }
+                rerotate<CD, 4>(x1, x2, co, so, cn, sn, z1, z2);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                  out.v[2 * v] = from_f32<KD>(z1[v]);
+                  out.v[2 * v + 1] = from_f32<KD>(z2[v]);
+                }
+              }
+              w = __builtin_bit_cast(V, out);
             }
-            rerotate<CD, 8>(x1, x2, co, so, cn, sn, z1, z2);
-            Pack<KS, 8> out;
-#pragma unroll
-            for (int v = 0; v < 8; ++v) out.v[v] = from_f32<KD>(lo ? z1[v] : z2[v]);
-            gstore(reinterpret_cast<V *>(dst + o), __builtin_bit_cast(V, out));
-          } else {
-            const int i0 = q * 4;
-            const Pack<CS, 4> co = load_half_pack<CS>(crow_o + i0);
-            const Pack<CS, 4> so = load_half_pack<CS>(crow_o + job.rot / 2 + i0);
-            const Pack<CS, 4> cn = load_half_pack<CS>(crow_n + i0);
-            const Pack<CS, 4> sn = load_half_pack<CS>(crow_n + job.rot / 2 + i0);
-            float x1[4], x2[4], z1[4], z2[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              x1[v] = to_f32<KD>(mine.v[2 * v]);
-              x2[v] = to_f32<KD>(mine.v[2 * v + 1]);
-            }
-            rerotate<CD, 4>(x1, x2, co, so, cn, sn, z1, z2);
-            Pack<KS, 8> out;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              out.v[2 * v] = from_f32<KD>(z1[v]);
-              out.v[2 * v + 1] = from_f32<KD>(z2[v]);
-            }
-            gstore(reinterpret_cast<V *>(dst + o), __builtin_bit_cast(V, out));
           }
+          gstore(reinterpret_cast<V *>(dst + o), w);
         }
       }
     }
@@ -335,8 +359,11 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
 }
 
 template <typename KD, typename CD, bool NEOX, bool ROPE>
-void launch_groups(const BlendJob &job, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((blend_layer_groups<KD, CD, NEOX, ROPE>), grid, dim3(kBlendThreads), 0, s, job);
+void launch_groups(const BlendJob &job, dim3 grid, bool host_objs, hipStream_t s) {
+  if (host_objs)
+    hipLaunchKernelGGL((blend_layer_groups<KD, CD, NEOX, ROPE, 1>), grid, dim3(kBlendThreads), 0, s, job);
+  else
+    hipLaunchKernelGGL((blend_layer_groups<KD, CD, NEOX, ROPE, 8>), grid, dim3(kBlendThreads), 0, s, job);
 }
 
 template <typename KD, typename CD, bool NEOX, bool ROPE>
@@ -358,15 +385,16 @@ void launch_blend_k(const BlendJob &job, dim3 grid, bool rope, int cache_dt, boo
 }
 
 template <typename KD>
-void launch_groups_k(const BlendJob &job, dim3 grid, bool rope, int cache_dt, bool neox, hipStream_t s) {
-  if (!rope) return launch_groups<KD, KD, true, false>(job, grid, s);
+void launch_groups_k(const BlendJob &job, dim3 grid, bool rope, int cache_dt, bool neox, bool host_objs,
+                     hipStream_t s) {
+  if (!rope) return launch_groups<KD, KD, true, false>(job, grid, host_objs, s);
   switch (cache_dt) {
-  case LMC_BF16: return neox ? launch_groups<KD, BF16, true, true>(job, grid, s)
-                             : launch_groups<KD, BF16, false, true>(job, grid, s);
-  case LMC_F16: return neox ? launch_groups<KD, F16, true, true>(job, grid, s)
-                            : launch_groups<KD, F16, false, true>(job, grid, s);
-  default: return neox ? launch_groups<KD, F32, true, true>(job, grid, s)
-                       : launch_groups<KD, F32, false, true>(job, grid, s);
+  case LMC_BF16: return neox ? launch_groups<KD, BF16, true, true>(job, grid, host_objs, s)
+                             : launch_groups<KD, BF16, false, true>(job, grid, host_objs, s);
+  case LMC_F16: return neox ? launch_groups<KD, F16, true, true>(job, grid, host_objs, s)
+                            : launch_groups<KD, F16, false, true>(job, grid, host_objs, s);
+  default: return neox ? launch_groups<KD, F32, true, true>(job, grid, host_objs, s)
+                       : launch_groups<KD, F32, false, true>(job, grid, host_objs, s);
   }
 }
 
@@ -510,13 +538,16 @@ extern "C" int lmc_blend_layer_to_paged(const lmc_tensor *objects, int32_t n_obj
         most = std::max(most, segs[b + k].count);
       }
       if (groups) {
-        // Reads of host memory: at most kBlendHostBlocks blocks in all.
-        int64_t gx = (most + kBlendThreads / 16 - 1) / (kBlendThreads / 16);
+        // A group per token (host objects) or per (token, plane) row (device
+        // objects); reads of host memory: at most kBlendHostBlocks blocks in
+        // all.
+        const int64_t items = host_objs ? most : (most + 3) / 4 * 8;
+        int64_t gx = (items + kBlendThreads / 16 - 1) / (kBlendThreads / 16);
         if (host_objs) gx = std::min<int64_t>(gx, std::max<int64_t>(1, kBlendHostBlocks / static_cast<int64_t>(n)));
         check(gx < (int64_t(1) << 31), "blend_layer_to_paged: too many tokens");
         const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n));
-        if (kdt == LMC_BF16) launch_groups_k<BF16>(job, grid, rope, cache_dt, is_neox != 0, s);
-        else launch_groups_k<F16>(job, grid, rope, cache_dt, is_neox != 0, s);
+        if (kdt == LMC_BF16) launch_groups_k<BF16>(job, grid, rope, cache_dt, is_neox != 0, host_objs, s);
+        else launch_groups_k<F16>(job, grid, rope, cache_dt, is_neox != 0, host_objs, s);
       } else {
         const int64_t gx = (2 * most + kBlendWaves - 1) / kBlendWaves;
         check(gx < (int64_t(1) << 31), "blend_layer_to_paged: too many tokens");

@@ -31,6 +31,9 @@ using FlashFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor
                         int32_t, void *);
 using RopeFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, int64_t,
                        const lmc_tensor *, int32_t, void *);
+using BlendFn = int (*)(const lmc_tensor *, int32_t, const int64_t *, const lmc_tensor *, int32_t,
+                        const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, const lmc_tensor *,
+                        int64_t, int32_t, int32_t, int32_t, void *);
 using ErrFn = const char *(*)();
 
 struct Table {
@@ -39,6 +42,7 @@ struct Table {
   FlashFn load_flash = nullptr;
   FlashFn reshape_flash = nullptr;
   RopeFn rope = nullptr;
+  BlendFn blend = nullptr;
   ErrFn last_error = nullptr;
 } g;
 
@@ -155,13 +159,56 @@ void rotary_embedding_k_fused(const at::Tensor &old_pos, const at::Tensor &new_p
   raise_for(g.rope(&a, &b, &k, head_size, &c, is_neox, stream_of(dev)));
 }
 
+// One layer of the CacheBlend retrieve in one kernel (lmc_blend_layer_to_paged).
+// Returns false when the library answers LMC_ERR_NOT_IMPLEMENTED (a shape
+// the fused kernel does not take), before any work, so the caller can run
+// the connector's own sequence; every other failure raises.
+bool blend_layer_to_paged(const std::vector<at::Tensor> &objs, const std::vector<int64_t> &token_starts,
+                          const py::object &caches_obj, const at::Tensor &slot_mapping,
+                          const c10::optional<at::Tensor> &old_positions,
+                          const c10::optional<at::Tensor> &new_positions,
+                          const c10::optional<at::Tensor> &cos_sin_cache, int64_t head_size, bool is_neox,
+                          int64_t kvcache_format_raw, bool vllm_two_major) {
+  check_bound();
+  if (objs.size() != token_starts.size()) throw py::value_error("memory_objs and token_starts differ in length");
+  const std::vector<at::Tensor> caches = normalize_kv_caches(caches_obj);
+  std::vector<lmc_tensor> cd, od;
+  cd.reserve(caches.size());
+  od.reserve(objs.size());
+  int dev = -1;
+  for (const auto &c : caches) {
+    cd.push_back(desc(c));
+    if (dev < 0 && c.is_cuda()) dev = c.get_device();
+  }
+  if (dev < 0) dev = slot_mapping.is_cuda() ? slot_mapping.get_device() : c10::hip::current_device();
+  for (const auto &o : objs) od.push_back(desc(o));
+  const bool rope = old_positions.has_value() || new_positions.has_value();
+  if (rope && !(old_positions.has_value() && new_positions.has_value() && cos_sin_cache.has_value()))
+    throw py::value_error("old_positions, new_positions and cos_sin_cache go together");
+  const lmc_tensor s = desc(slot_mapping);
+  lmc_tensor a{}, b{}, c{};
+  if (rope) {
+    a = desc(*old_positions);
+    b = desc(*new_positions);
+    c = desc(*cos_sin_cache);
+  }
+  const int status = g.blend(od.data(), static_cast<int32_t>(od.size()), token_starts.data(), cd.data(),
+                             static_cast<int32_t>(cd.size()), &s, rope ? &a : nullptr, rope ? &b : nullptr,
+                             rope ? &c : nullptr, head_size, is_neox, static_cast<int32_t>(kvcache_format_raw),
+                             vllm_two_major, stream_of(dev));
+  if (status == LMC_ERR_NOT_IMPLEMENTED) return false;
+  raise_for(status);
+  return true;
+}
+
 void bind(uintptr_t multi, uintptr_t single, uintptr_t load_flash, uintptr_t reshape_flash,
-          uintptr_t rope, uintptr_t last_error) {
+          uintptr_t rope, uintptr_t blend, uintptr_t last_error) {
   g.multi = reinterpret_cast<MultiFn>(multi);
   g.single = reinterpret_cast<SingleFn>(single);
   g.load_flash = reinterpret_cast<FlashFn>(load_flash);
   g.reshape_flash = reinterpret_cast<FlashFn>(reshape_flash);
   g.rope = reinterpret_cast<RopeFn>(rope);
+  g.blend = reinterpret_cast<BlendFn>(blend);
   g.last_error = reinterpret_cast<ErrFn>(last_error);
 }
 
@@ -184,4 +231,5 @@ PYBIND11_MODULE(_c_ops_ext, m) {
           flash(g.reshape_flash, kv, kc, vc, s, layer);
         });
   m.def("rotary_embedding_k_fused", &rotary_embedding_k_fused);
+  m.def("blend_layer_to_paged", &blend_layer_to_paged);
 }

@@ -43,6 +43,7 @@ try:
         _addr("lmc_load_and_reshape_flash"),
         _addr("lmc_reshape_and_cache_back_flash"),
         _addr("lmc_rotary_embedding_k_fused"),
+        _addr("lmc_blend_layer_to_paged"),
         _addr("lmc_last_error"),
     )
 except ImportError:
@@ -433,6 +434,18 @@ def blend_layer_to_paged(
     objs = list(memory_objs)
     if len(objs) != len(token_starts):
         raise ValueError("memory_objs and token_starts differ in length")
+    rope = old_positions is not None or new_positions is not None
+    if rope and (old_positions is None or new_positions is None or cos_sin_cache is None):
+        raise ValueError("old_positions, new_positions and cos_sin_cache go together")
+    if _ext is not None:
+        done = _ext.blend_layer_to_paged(
+            objs, [int(x) for x in token_starts], vllm_kv_caches, slot_mapping, old_positions, new_positions,
+            cos_sin_cache, int(head_size), bool(is_neox), int(kvcache_format_raw), bool(vllm_two_major))
+        if not done:
+            _blend_connector_sequence(objs, token_starts, vllm_kv_caches, slot_mapping, old_positions,
+                                      new_positions, cos_sin_cache, head_size, is_neox, kvcache_format_raw,
+                                      vllm_two_major)
+        return
     dev = _device_index(*(caches + [slot_mapping]))
     carr = (_lib.LmcTensor * max(len(caches), 1))()
     for i, c in enumerate(caches):
@@ -442,9 +455,6 @@ def blend_layer_to_paged(
         oarr[i] = _desc(o)
     starts = (ctypes.c_int64 * max(len(objs), 1))(*[int(x) for x in token_starts])
     s = _desc(slot_mapping)
-    rope = old_positions is not None or new_positions is not None
-    if rope and (old_positions is None or new_positions is None or cos_sin_cache is None):
-        raise ValueError("old_positions, new_positions and cos_sin_cache go together")
     a = _desc(old_positions) if rope else None
     b = _desc(new_positions) if rope else None
     c = _desc(cos_sin_cache) if rope else None
@@ -456,7 +466,16 @@ def blend_layer_to_paged(
     if status != _lib.ERR_NOT_IMPLEMENTED:
         _run(status)
         return
-    # The connector's own sequence (npu_connectors.py:597-680), on device.
+    _blend_connector_sequence(objs, token_starts, vllm_kv_caches, slot_mapping, old_positions, new_positions,
+                              cos_sin_cache, head_size, is_neox, kvcache_format_raw, vllm_two_major)
+
+
+def _blend_connector_sequence(objs, token_starts, vllm_kv_caches, slot_mapping, old_positions, new_positions,
+                              cos_sin_cache, head_size, is_neox, kvcache_format_raw, vllm_two_major) -> None:
+    """The connector's own sequence (npu_connectors.py:597-680), on device,
+    for shapes the fused kernel does not take."""
+    caches = _normalize_kv_caches(vllm_kv_caches)
+    rope = old_positions is not None
     k0 = caches[0]
     width = k0.shape[-2] * k0.shape[-1]
     n_tok = int(slot_mapping.numel())
