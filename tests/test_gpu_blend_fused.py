@@ -229,3 +229,11 @@ def test_blend_layer_graph_replays(ops):
         torch.cuda.synchronize()
         for g, w in zip(gpu, want):
             assert np.array_equal(to_bytes(g), w.data), f"replay {rep}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_blend_layer_through_ctypes(ops, monkeypatch, dtype):
+    """The same op with the C++ binding absent (the ctypes path), fused
+    (bf16) and through the connector's sequence (fp32)."""
+    monkeypatch.setattr(ops, "_ext", None)
+    _run_case(ops, 2, False, dtype, "pinned", "i64", True, D, "gaps", seed=43)
