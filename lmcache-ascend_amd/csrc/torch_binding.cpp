@@ -34,6 +34,8 @@ using RopeFn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor 
 using BlendFn = int (*)(const lmc_tensor *, int32_t, const int64_t *, const lmc_tensor *, int32_t,
                         const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, const lmc_tensor *,
                         int64_t, int32_t, int32_t, int32_t, void *);
+using CdfFn = int (*)(const lmc_tensor *, int32_t, const lmc_tensor *, void *);
+using Codec4Fn = int (*)(const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, const lmc_tensor *, void *);
 using ErrFn = const char *(*)();
 
 struct Table {
@@ -43,6 +45,9 @@ struct Table {
   FlashFn reshape_flash = nullptr;
   RopeFn rope = nullptr;
   BlendFn blend = nullptr;
+  CdfFn cdf = nullptr;
+  Codec4Fn encode = nullptr;
+  Codec4Fn decode = nullptr;
   ErrFn last_error = nullptr;
 } g;
 
@@ -201,14 +206,39 @@ bool blend_layer_to_paged(const std::vector<at::Tensor> &objs, const std::vector
   return true;
 }
 
+// CacheGen (csrc/cachegen_kernels.cpp:17-155).  calculate_cdf returns a
+// zero-initialised int16 [L, C, n_bins + 1] tensor, as the reference does.
+at::Tensor calculate_cdf(const at::Tensor &input, int64_t n_bins) {
+  check_bound();
+  if (!input.is_cuda()) throw std::runtime_error("calculate_cdf: input must be a GPU tensor");
+  if (input.dim() != 3) throw std::runtime_error("input must be [layers, tokens, channels]");
+  at::Tensor out = at::zeros({input.size(0), input.size(2), n_bins + 1},
+                             input.options().dtype(at::kShort));
+  const lmc_tensor a = desc(input), o = desc(out);
+  raise_for(g.cdf(&a, static_cast<int32_t>(n_bins), &o, stream_of(input.get_device())));
+  return out;
+}
+
+void codec4(Codec4Fn fn, const at::Tensor &t0, const at::Tensor &t1, const at::Tensor &t2,
+            const at::Tensor &t3, const at::Tensor &dev_of) {
+  check_bound();
+  const int dev = dev_of.is_cuda() ? dev_of.get_device() : c10::hip::current_device();
+  const lmc_tensor a = desc(t0), b = desc(t1), c = desc(t2), d = desc(t3);
+  raise_for(fn(&a, &b, &c, &d, stream_of(dev)));
+}
+
 void bind(uintptr_t multi, uintptr_t single, uintptr_t load_flash, uintptr_t reshape_flash,
-          uintptr_t rope, uintptr_t blend, uintptr_t last_error) {
+          uintptr_t rope, uintptr_t blend, uintptr_t cdf, uintptr_t encode, uintptr_t decode,
+          uintptr_t last_error) {
   g.multi = reinterpret_cast<MultiFn>(multi);
   g.single = reinterpret_cast<SingleFn>(single);
   g.load_flash = reinterpret_cast<FlashFn>(load_flash);
   g.reshape_flash = reinterpret_cast<FlashFn>(reshape_flash);
   g.rope = reinterpret_cast<RopeFn>(rope);
   g.blend = reinterpret_cast<BlendFn>(blend);
+  g.cdf = reinterpret_cast<CdfFn>(cdf);
+  g.encode = reinterpret_cast<Codec4Fn>(encode);
+  g.decode = reinterpret_cast<Codec4Fn>(decode);
   g.last_error = reinterpret_cast<ErrFn>(last_error);
 }
 
@@ -232,4 +262,12 @@ PYBIND11_MODULE(_c_ops_ext, m) {
         });
   m.def("rotary_embedding_k_fused", &rotary_embedding_k_fused);
   m.def("blend_layer_to_paged", &blend_layer_to_paged);
+  m.def("calculate_cdf", &calculate_cdf);
+  m.def("encode_fast_new", [](const at::Tensor &cdf, const at::Tensor &sym, at::Tensor &out, at::Tensor &lens) {
+    codec4(g.encode, cdf, sym, out, lens, sym);
+  });
+  m.def("decode_fast_prefsum",
+        [](const at::Tensor &cdf, const at::Tensor &bytes, const at::Tensor &lens, at::Tensor &out) {
+          codec4(g.decode, cdf, bytes, lens, out, bytes);
+        });
 }

@@ -44,6 +44,9 @@ try:
         _addr("lmc_reshape_and_cache_back_flash"),
         _addr("lmc_rotary_embedding_k_fused"),
         _addr("lmc_blend_layer_to_paged"),
+        _addr("lmc_calculate_cdf"),
+        _addr("lmc_encode_fast_new"),
+        _addr("lmc_decode_fast_prefsum"),
         _addr("lmc_last_error"),
     )
 except ImportError:
@@ -369,6 +372,8 @@ def reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping
 def calculate_cdf(input: torch.Tensor, n_bins: int) -> torch.Tensor:
     """csrc/cachegen_kernels.cpp:119-155: int16 [L, C, n_bins + 1] CDF of the
     [L, T, C] symbols; the output is zero-initialised like the reference's."""
+    if _ext is not None:
+        return _ext.calculate_cdf(input, int(n_bins))
     if not input.is_cuda:
         raise RuntimeError("calculate_cdf: input must be a GPU tensor")
     L, _, C = input.shape
@@ -381,6 +386,9 @@ def calculate_cdf(input: torch.Tensor, n_bins: int) -> torch.Tensor:
 
 def encode_fast_new(cdf, input_sym, output_buffer, output_lengths) -> None:
     """csrc/cachegen_kernels.cpp:17-58."""
+    if _ext is not None:
+        _ext.encode_fast_new(cdf, input_sym, output_buffer, output_lengths)
+        return
     dev = _device_index(input_sym)
     c, i, o, n = _desc(cdf), _desc(input_sym), _desc(output_buffer), _desc(output_lengths)
     _run(_L.lmc_encode_fast_new(_ref(c), _ref(i), _ref(o), _ref(n), _stream(dev)))
@@ -393,6 +401,9 @@ def decode_fast_new(cdf, bytestreams, lengths, output) -> None:
 
 def decode_fast_prefsum(cdf, bytestreams, lengths, output) -> None:
     """csrc/cachegen_kernels.cpp:67-112; lengths are inclusive prefix sums."""
+    if _ext is not None:
+        _ext.decode_fast_prefsum(cdf, bytestreams, lengths, output)
+        return
     dev = _device_index(bytestreams)
     c, b, n, o = _desc(cdf), _desc(bytestreams), _desc(lengths), _desc(output)
     _run(_L.lmc_decode_fast_prefsum(_ref(c), _ref(b), _ref(n), _ref(o), _stream(dev)))

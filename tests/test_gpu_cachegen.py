@@ -326,3 +326,26 @@ def test_decode_valid_streams_across_lengths(ops, T, C):
                             torch.from_numpy(pref).to(DEV), out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), syms)
+
+
+def test_codec_through_ctypes(ops, monkeypatch):
+    """calculate_cdf, encode and decode with the C++ binding absent (the
+    ctypes path), against the oracle."""
+    monkeypatch.setattr(ops, "_ext", None)
+    syms = _kv_chunk_symbols(L=2, T=200, C=192, seed=5)
+    d = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d, 32)
+    want_cdf = oc.calculate_cdf(syms, 32)
+    out = torch.zeros((syms.shape[0], syms.shape[2], MAX_TOKENS_PER_CHUNK), dtype=torch.uint8, device=DEV)
+    lens = torch.zeros((syms.shape[0], syms.shape[2]), dtype=torch.int32, device=DEV)
+    ops.encode_fast_new(cdf, d, out, lens)
+    want_out, want_len = oc.encode(want_cdf, syms, MAX_TOKENS_PER_CHUNK)
+    torch.cuda.synchronize()
+    assert np.array_equal(cdf.cpu().numpy(), want_cdf)
+    assert np.array_equal(lens.cpu().numpy(), want_len)
+    assert np.array_equal(out.cpu().numpy(), want_out)
+    stream, pref = oc.concat_streams(want_out, want_len)
+    dec = torch.zeros_like(d)
+    ops.decode_fast_prefsum(cdf, torch.from_numpy(stream).to(DEV), torch.from_numpy(pref).to(DEV), dec)
+    torch.cuda.synchronize()
+    assert torch.equal(dec, d)
