@@ -206,13 +206,14 @@ bool blend_layer_to_paged(const std::vector<at::Tensor> &objs, const std::vector
   return true;
 }
 
-// CacheGen (csrc/cachegen_kernels.cpp:17-155).  calculate_cdf returns a
-// zero-initialised int16 [L, C, n_bins + 1] tensor, as the reference does.
+// CacheGen (csrc/cachegen_kernels.cpp:17-155).  calculate_cdf returns an
+// int16 [L, C, n_bins + 1] tensor; the reference zero-fills it first, but
+// the kernels write every entry of it, so it is allocated without a fill.
 at::Tensor calculate_cdf(const at::Tensor &input, int64_t n_bins) {
   check_bound();
   if (!input.is_cuda()) throw std::runtime_error("calculate_cdf: input must be a GPU tensor");
   if (input.dim() != 3) throw std::runtime_error("input must be [layers, tokens, channels]");
-  at::Tensor out = at::zeros({input.size(0), input.size(2), n_bins + 1},
+  at::Tensor out = at::empty({input.size(0), input.size(2), n_bins + 1},
                              input.options().dtype(at::kShort));
   const lmc_tensor a = desc(input), o = desc(out);
   raise_for(g.cdf(&a, static_cast<int32_t>(n_bins), &o, stream_of(input.get_device())));

@@ -371,13 +371,14 @@ def reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping
 
 def calculate_cdf(input: torch.Tensor, n_bins: int) -> torch.Tensor:
     """csrc/cachegen_kernels.cpp:119-155: int16 [L, C, n_bins + 1] CDF of the
-    [L, T, C] symbols; the output is zero-initialised like the reference's."""
+    [L, T, C] symbols.  The reference zero-fills the output first; the
+    kernels write every entry of it, so it is allocated without a fill."""
     if _ext is not None:
         return _ext.calculate_cdf(input, int(n_bins))
     if not input.is_cuda:
         raise RuntimeError("calculate_cdf: input must be a GPU tensor")
     L, _, C = input.shape
-    out = torch.zeros((L, C, int(n_bins) + 1), dtype=torch.int16, device=input.device)
+    out = torch.empty((L, C, int(n_bins) + 1), dtype=torch.int16, device=input.device)
     dev = input.device.index
     a, o = _desc(input), _desc(out)
     _run(_L.lmc_calculate_cdf(_ref(a), int(n_bins), _ref(o), _stream(dev)))

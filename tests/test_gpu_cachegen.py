@@ -349,3 +349,18 @@ def test_codec_through_ctypes(ops, monkeypatch):
     ops.decode_fast_prefsum(cdf, torch.from_numpy(stream).to(DEV), torch.from_numpy(pref).to(DEV), dec)
     torch.cuda.synchronize()
     assert torch.equal(dec, d)
+
+
+@pytest.mark.parametrize("T,C,nb", [(256, 1024, 32), (100, 100, 17), (300, 70, 32), (1, 64, 64)])
+def test_calculate_cdf_writes_every_entry(ops, T, C, nb):
+    """calculate_cdf allocates its output without a fill: the kernels must
+    write every entry.  Called through the C ABI into an output holding
+    -1 everywhere (tiled kernel for T <= 256, one lane per stream above)."""
+    rng = np.random.default_rng(T + C + nb)
+    syms = rng.integers(0, nb, size=(3, T, C), dtype=np.uint8)
+    d = torch.from_numpy(syms).to(DEV)
+    out = torch.full((3, C, nb + 1), -1, dtype=torch.int16, device=DEV)
+    a, o = ops._desc(d), ops._desc(out)
+    ops._run(ops._L.lmc_calculate_cdf(ops._ref(a), nb, ops._ref(o), ops._stream(0)))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), oc.calculate_cdf(syms, nb))
