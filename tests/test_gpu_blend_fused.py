@@ -129,10 +129,19 @@ def test_blend_layer_separate_vs_oracle(ops, objs_on, rope_kind, layout):
     _run_case(ops, 2, False, torch.bfloat16, objs_on, rope_kind, True, D, layout, seed=11)
 
 
+@pytest.mark.parametrize("objs_on", ["pinned", "device"])
 @pytest.mark.parametrize("two_major", [True, False])
 @pytest.mark.parametrize("neox", [True, False])
-def test_blend_layer_merged_vs_oracle(ops, two_major, neox):
-    _run_case(ops, 1, two_major, torch.bfloat16, "pinned", "i64", neox, D, "gaps", seed=13 + two_major + 2 * neox)
+def test_blend_layer_merged_vs_oracle(ops, objs_on, two_major, neox):
+    _run_case(ops, 1, two_major, torch.bfloat16, objs_on, "i64", neox, D, "gaps", seed=13 + two_major + 2 * neox)
+
+
+@pytest.mark.parametrize("objs_on", ["pinned", "device"])
+@pytest.mark.parametrize("neox", [True, False])
+def test_blend_layer_fp16_keys_whole_heads(ops, objs_on, neox):
+    """fp16 keys rotated whole (the 16-lane group kernel) with a bf16
+    cos/sin cache, from pinned and from device objects."""
+    _run_case(ops, 2, False, torch.float16, objs_on, "i32", neox, D, "dense", seed=47 + neox)
 
 
 @pytest.mark.parametrize("neox", [True, False])
@@ -237,3 +246,33 @@ def test_blend_layer_through_ctypes(ops, monkeypatch, dtype):
     (bf16) and through the connector's sequence (fp32)."""
     monkeypatch.setattr(ops, "_ext", None)
     _run_case(ops, 2, False, dtype, "pinned", "i64", True, D, "gaps", seed=43)
+
+
+@pytest.mark.parametrize("rope_kind", ["none", "i64"])
+def test_blend_layer_grid_stride_over_a_long_object(ops, rope_kind):
+    """One pinned object of 9000 tokens: more tokens than the capped grid for
+    host objects covers in one pass, so groups stride over the segment.
+    Tokens past the cache's 768 slots get -1 (skipped)."""
+    gen = torch.Generator().manual_seed(53)
+    caches = _caches(2, False, torch.bfloat16, gen)
+    gpu = tuple(c.to(DEV) for c in caches)
+    n_tok = 9000
+    obj = torch.randn((2, n_tok, W), generator=gen).to(torch.bfloat16)
+    slots = torch.full((n_tok,), -1, dtype=torch.int64)
+    perm = torch.tensor(sample_slots(NB * BS, NB * BS, seed=53), dtype=torch.int64)
+    pick = torch.randperm(n_tok, generator=gen)[: NB * BS]
+    slots[pick] = perm
+    rope, kwargs = None, {}
+    if rope_kind != "none":
+        max_pos = 12000
+        cache = orope.cos_sin_cache(max_pos, D, 500000.0).to(torch.bfloat16)
+        old = torch.arange(n_tok, dtype=torch.int64)
+        new = old + 7
+        rope = (old, new, cache, D, True)
+        kwargs = dict(old_positions=old.to(DEV), new_positions=new.to(DEV), cos_sin_cache=cache.to(DEV),
+                      head_size=D, is_neox=True)
+    want = _expected(caches, 2, False, [obj], [0], n_tok, slots, rope)
+    ops.blend_layer_to_paged([obj.pin_memory()], [0], gpu, slots.to(DEV), kvcache_format_raw=2, **kwargs)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(to_bytes(g), w.data)
