@@ -223,6 +223,7 @@ def decode_chunk(chunk: CacheGenChunk) -> torch.Tensor:
     streams = chunk.streams.to(dev)
     if streams.numel() == 0:  # the op needs an addressable buffer
         streams = torch.zeros(1, dtype=torch.uint8, device=dev)
-    out = torch.zeros((L, T, C), dtype=torch.uint8, device=dev)
+    # decode_fast_prefsum writes all T symbols of every stream.
+    out = torch.empty((L, T, C), dtype=torch.uint8, device=dev)
     c_ops.decode_fast_prefsum(chunk.cdf, streams, prefix, out)
     return out
