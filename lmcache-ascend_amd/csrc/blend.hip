@@ -48,6 +48,12 @@ constexpr int kVP = 8;            // rotation pairs per lane group
 #endif
 constexpr int kBlendHostBlocks = LMC_BLEND_HOST_BLOCKS;  // grid cap for reads of host memory
 
+// Rows are stored into the paged caches (device memory) with the streaming
+// hint.  Measured on MI355X, one Llama-3-8B-shape layer (kernel times, two
+// runs each): device objects 10.4-10.6 -> 9.3 us with re-rotation and
+// 6.4 -> 5.9 us without; pinned objects unchanged (0.300 ms).
+template <typename T> __device__ __forceinline__ void bst(T *p, T v) { gstore_nt(p, v); }
+
 struct BlendSeg {
   uint64_t src;          // memory object (kernel-visible), 0 for uncovered tokens
   int64_t tok0;          // first token (index into slots / positions)
@@ -88,7 +94,7 @@ template <typename P> __device__ __forceinline__ P load_pack(const void *p) {
 template <typename P> __device__ __forceinline__ void store_pack(void *p, const P &v) {
   const Words<sizeof(P) / 16> r = __builtin_bit_cast(Words<sizeof(P) / 16>, v);
 #pragma unroll
-  for (int k = 0; k < static_cast<int>(sizeof(P) / 16); ++k) gstore(static_cast<u32x4 *>(p) + k, r.w[k]);
+  for (int k = 0; k < static_cast<int>(sizeof(P) / 16); ++k) bst(static_cast<u32x4 *>(p) + k, r.w[k]);
 }
 
 // Four cos/sin values (8 bytes of bf16 / fp16, 16 of fp32), through the
@@ -135,7 +141,7 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_rows(const BlendJob
   if (sg.src == 0) {  // a token no object covers: a zero row
     const V z = {0u, 0u, 0u, 0u};
     for (int64_t o = static_cast<int64_t>(lane) * 16; o < rb; o += 64 * 16)
-      gstore(reinterpret_cast<V *>(dst + o), z);
+      bst(reinterpret_cast<V *>(dst + o), z);
     return;
   }
   const uint8_t *src = reinterpret_cast<const uint8_t *>(sg.src) + p * sg.plane_bytes + i * rb;
@@ -202,7 +208,7 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_rows(const BlendJob
           const int h = q / pass;
           const int64_t o = (static_cast<int64_t>(h) * job.head_size + job.rot) * static_cast<int64_t>(sizeof(KS)) +
                             static_cast<int64_t>(q - h * pass) * 16;
-          gstore(reinterpret_cast<V *>(dst + o), gload(reinterpret_cast<const V *>(src + o)));
+          bst(reinterpret_cast<V *>(dst + o), gload(reinterpret_cast<const V *>(src + o)));
         }
         return;
       }
@@ -214,10 +220,10 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_rows(const BlendJob
   const int64_t o0 = static_cast<int64_t>(lane) * 16, o1 = o0 + 64 * 16;
   if (o0 < rb) v[0] = gload(reinterpret_cast<const V *>(src + o0));
   if (o1 < rb) v[1] = gload(reinterpret_cast<const V *>(src + o1));
-  if (o0 < rb) gstore(reinterpret_cast<V *>(dst + o0), v[0]);
-  if (o1 < rb) gstore(reinterpret_cast<V *>(dst + o1), v[1]);
+  if (o0 < rb) bst(reinterpret_cast<V *>(dst + o0), v[0]);
+  if (o1 < rb) bst(reinterpret_cast<V *>(dst + o1), v[1]);
   for (int64_t o = o0 + 2 * 64 * 16; o < rb; o += 64 * 16)
-    gstore(reinterpret_cast<V *>(dst + o), gload(reinterpret_cast<const V *>(src + o)));
+    bst(reinterpret_cast<V *>(dst + o), gload(reinterpret_cast<const V *>(src + o)));
 }
 
 // Tokens by 16-lane groups, for rows without re-rotation and for K rows
@@ -295,7 +301,7 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
                      in_blk * pd.row_pitch;
       if (sg.src == 0) {  // a token no object covers: zero rows
         const V z = {0u, 0u, 0u, 0u};
-        for (int64_t o = static_cast<int64_t>(q) * 16; o < rb; o += 256) gstore(reinterpret_cast<V *>(dst + o), z);
+        for (int64_t o = static_cast<int64_t>(q) * 16; o < rb; o += 256) bst(reinterpret_cast<V *>(dst + o), z);
         continue;
       }
       const uint8_t *src = reinterpret_cast<const uint8_t *>(sg.src) + p * sg.plane_bytes + i * rb;
@@ -351,7 +357,7 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
               w = __builtin_bit_cast(V, out);
             }
           }
-          gstore(reinterpret_cast<V *>(dst + o), w);
+          bst(reinterpret_cast<V *>(dst + o), w);
         }
       }
     }
