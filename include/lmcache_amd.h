@@ -135,8 +135,12 @@ int lmc_fused_multi_layer_kv_transfer(
  * staging device is `paged_device` (the current device when negative).  A
  * store zeroes the staging bytes first (a fill kernel), so rows of skipped
  * slots arrive in `key_value` as zeros, as with a zeroed staging_cache.
- * Every call on one GPU shares that GPU's area: calls that overlap on one GPU
- * (on different streams, or from different threads) race. */
+ * Every call on one GPU shares that GPU's area.  Eager calls are ordered:
+ * each call's stream waits for the previous call's work (an event recorded
+ * per GPU), whatever stream or thread made it.  Calls enqueued under HIP
+ * graph capture skip that wait, so a graph replay that overlaps another
+ * call on the same GPU races with it.  The area lives in its own code
+ * object, reserved on a GPU only once this entry point has run there. */
 #define LMC_NOALLOC_STAGING_BYTES (64ll << 20)
 int lmc_fused_multi_layer_kv_transfer_noalloc(
     const lmc_tensor *key_value, const lmc_tensor *key_value_ptrs,

@@ -20,7 +20,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "lmcache_amd", "liblmcache_amd.so")
-SOURCES = ["kv_transfer.hip", "kv_direct.hip", "kv_sparse_graph.hip", "indexer_c8.hip", "cachegen.hip", "rope.hip",
+SOURCES = ["kv_transfer.hip", "kv_noalloc.hip", "kv_direct.hip", "kv_sparse_graph.hip", "indexer_c8.hip", "cachegen.hip", "rope.hip",
            "host_mem.cpp", "host_shm.cpp", "dma_copy.hip", "blend.hip"]
 ARCH = "gfx950"
 

@@ -31,8 +31,7 @@
 // (csrc/graph/sparse_graph_kernel.cpp:45-48, tools/cpu_vllm_runtime.py:
 // 379-380); skipping is the superset.
 #include "kv_geom.h"
-
-#include <mutex>
+#include "kv_fused.h"
 
 namespace lmc {
 
@@ -1139,35 +1138,6 @@ int64_t fused_required_size(int fmt, bool use_mla, int64_t L, int64_t T,
   }
 }
 
-// Staging area of lmc_fused_multi_layer_kv_transfer_noalloc: one memory
-// object of up to LMC_NOALLOC_STAGING_BYTES, allocated per GPU when the
-// code object loads and held until the process ends.  Host code never uses
-// this name as an address: it is resolved once per device with
-// hipGetSymbolAddress (noalloc_staging below).
-static __device__ __align__(256) uint8_t scratch[LMC_NOALLOC_STAGING_BYTES];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_noalloc_mu;
-uint8_t *g_noalloc_ptr[kMaxDevices] = {};
-
-// Device address of `device`'s staging area; resolved on the first call per
-// device, with that device current.
-uint8_t *noalloc_staging(int device) {
-  check(device >= 0 && device < kMaxDevices,
-        "fused_multi_layer_kv_transfer_noalloc: device " +
-            std::to_string(device) + " out of range");
-  std::lock_guard<std::mutex> lock(g_noalloc_mu);
-  if (g_noalloc_ptr[device] == nullptr) {
-    DeviceGuard guard(device);
-    void *p = nullptr;
-    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
-              "hipGetSymbolAddress(staging area)");
-    check(p != nullptr, "hipGetSymbolAddress returned a null staging area");
-    g_noalloc_ptr[device] = static_cast<uint8_t *>(p);
-  }
-  return g_noalloc_ptr[device];
-}
-
 // Zeroes `n16` 16-byte words from `p` (a fill kernel, not hipMemsetAsync, so
 // the call can be recorded into a HIP graph).
 __global__ void __launch_bounds__(256) zero_words(u32x4 *p, int64_t n16) {
@@ -1177,11 +1147,7 @@ __global__ void __launch_bounds__(256) zero_words(u32x4 *p, int64_t n16) {
     gstore(p + i, z);
 }
 
-// fused_multi_layer_kv_transfer through a staging buffer of `capacity`
-// bytes at `stg_data` on device `stg_device` (csrc/mem_kernels.cpp:113-213):
-// H2D copy into the staging buffer before a load, the gather/scatter against
-// it, D2H copy out of it after a store.  `clear_before_store` zeroes the
-// staging bytes of a store first, so rows of skipped slots leave as zeros.
+// Declared, with its contract, in kv_fused.h.
 void fused_transfer(const lmc_tensor &kv, uint8_t *stg_data, int stg_device,
                     int64_t capacity, const char *too_small,
                     bool clear_before_store, const lmc_tensor *key_value_ptrs,
@@ -1283,27 +1249,6 @@ int lmc_fused_multi_layer_kv_transfer(
     fused_transfer(kv, static_cast<uint8_t *>(stg.data), stg.device,
                    nbytes(stg), "staging_cache size insufficient", false,
                    key_value_ptrs, slot_mapping, paged_device,
-                   page_buffer_size, direction != 0, use_mla != 0,
-                   kvcache_format, k_hidden_dims, v_hidden_dims,
-                   dsa_hidden_dims, as_stream(stream));
-  });
-}
-
-int lmc_fused_multi_layer_kv_transfer_noalloc(
-    const lmc_tensor *key_value, const lmc_tensor *key_value_ptrs,
-    const lmc_tensor *slot_mapping, int32_t paged_device,
-    int64_t page_buffer_size, int32_t direction, int32_t use_mla,
-    int32_t kvcache_format, int64_t k_hidden_dims, int64_t v_hidden_dims,
-    int64_t dsa_hidden_dims, void *stream) {
-  return guarded([&] {
-    const lmc_tensor &kv = deref(key_value, "key_value");
-    int device = paged_device;
-    if (device < 0) hip_check(hipGetDevice(&device), "hipGetDevice");
-    uint8_t *stg = noalloc_staging(device);
-    fused_transfer(kv, stg, device, LMC_NOALLOC_STAGING_BYTES,
-                   "fused_multi_layer_kv_transfer_noalloc: the transfer "
-                   "exceeds the library's staging area",
-                   true, key_value_ptrs, slot_mapping, device,
                    page_buffer_size, direction != 0, use_mla != 0,
                    kvcache_format, k_hidden_dims, v_hidden_dims,
                    dsa_hidden_dims, as_stream(stream));
