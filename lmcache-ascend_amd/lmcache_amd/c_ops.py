@@ -261,8 +261,10 @@ def fused_multi_layer_kv_transfer_noalloc(
     callers that cannot allocate device memory: the library stages through
     its own NOALLOC_STAGING_BYTES area on the cache device and allocates
     nothing.  A store zeroes the staging bytes first, so rows of skipped
-    slots arrive as zeros.  Calls overlapping on one GPU share that area and
-    race."""
+    slots arrive as zeros.  Every call on one GPU shares that area: eager
+    calls are ordered across streams and threads (each waits for the
+    previous call's work), calls captured into a HIP graph are not, so a
+    replay overlapping another call on the same GPU races with it."""
     dev = _device_index(paged_memory_device, key_value_ptrs)
     a, p, s = _desc(key_value), _desc(key_value_ptrs), _desc(slot_mapping)
     _run(
@@ -485,13 +487,17 @@ def blend_layer_to_paged(
 def _blend_connector_sequence(objs, token_starts, vllm_kv_caches, slot_mapping, old_positions, new_positions,
                               cos_sin_cache, head_size, is_neox, kvcache_format_raw, vllm_two_major) -> None:
     """The connector's own sequence (npu_connectors.py:597-680), on device,
-    for shapes the fused kernel does not take."""
+    for shapes the fused kernel does not take.  The layer buffer lives on
+    the caches' device; a slot mapping in pinned host memory, which the
+    fused entry point accepts, is copied there first."""
     caches = _normalize_kv_caches(vllm_kv_caches)
     rope = old_positions is not None
     k0 = caches[0]
+    dev = k0.device
+    slot_mapping = slot_mapping.to(dev)
     width = k0.shape[-2] * k0.shape[-1]
     n_tok = int(slot_mapping.numel())
-    buf = torch.zeros((2, n_tok, width), dtype=k0.dtype, device=slot_mapping.device)
+    buf = torch.zeros((2, n_tok, width), dtype=k0.dtype, device=dev)
     for o, st in zip(objs, token_starts):
         buf[:, int(st):int(st) + o.shape[1]].copy_(o, non_blocking=True)
     if rope:

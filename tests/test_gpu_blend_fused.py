@@ -78,7 +78,8 @@ def _expected(caches, fmt, two_major, objs, starts, n_tok, slots, rope):
     return want
 
 
-def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout, seed, slot_dtype=torch.int64):
+def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout, seed, slot_dtype=torch.int64,
+              slots_on="device"):
     gen = torch.Generator().manual_seed(seed)
     caches = _caches(fmt, two_major, dtype, gen)
     gpu = caches.to(DEV) if isinstance(caches, torch.Tensor) else tuple(c.to(DEV) for c in caches)
@@ -113,7 +114,9 @@ def _run_case(ops, fmt, two_major, dtype, objs_on, rope_kind, neox, rot, layout,
         kwargs = dict(old_positions=old.to(pdt).to(DEV), new_positions=new.to(pdt).to(DEV),
                       cos_sin_cache=cache.to(DEV), head_size=D, is_neox=neox)
     want = _expected(caches, fmt, two_major, objs, starts, n_tok, slots, rope)
-    ops.blend_layer_to_paged(dobjs, starts, gpu, slots.to(slot_dtype).to(DEV), kvcache_format_raw=fmt,
+    sl = slots.to(slot_dtype)
+    sl = sl.pin_memory() if slots_on == "pinned" else sl.to(DEV)
+    ops.blend_layer_to_paged(dobjs, starts, gpu, sl, kvcache_format_raw=fmt,
                              vllm_two_major=two_major,
                              **kwargs)
     torch.cuda.synchronize()
@@ -155,6 +158,14 @@ def test_blend_layer_fp32_keys_take_the_connector_sequence(ops):
     """fp32 caches are outside the fused kernel: the op runs the connector's
     own sequence with this library's ops, with the same bytes."""
     _run_case(ops, 2, False, torch.float32, "device", "i64", True, D, "gaps", seed=19)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_blend_layer_slots_in_pinned_host_memory(ops, dtype):
+    """A slot mapping in pinned host memory, which the entry point accepts:
+    the fused kernel reads it over PCIe (bf16), and the connector sequence
+    (fp32 keys) copies it to the caches' device first."""
+    _run_case(ops, 2, False, dtype, "pinned", "i64", True, D, "gaps", seed=53, slots_on="pinned")
 
 
 def test_blend_layer_without_objects_zeroes_every_named_slot(ops):
