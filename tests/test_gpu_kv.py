@@ -601,6 +601,46 @@ def test_llama8b_shape_full_size_round_trip(ops):
     assert checksum_before == checksum_after
 
 
+def test_llama8b_shape_full_size_pinned_round_trip(ops):
+    """The same Llama-3-8B-shape batch with its 16 memory objects in
+    page-locked host memory, one batched launch per direction (the
+    pinned-host mode of the benchmark, kernel reads and writes over PCIe).
+    Store: every object equals torch's index_select gather of all 32 layers
+    and both planes.  Retrieve into the zeroed touched slots restores them
+    and leaves the other rows' checksums unchanged."""
+    L, NB, BS, H, D = 32, 2048, 128, 8, 128
+    W = H * D
+    pbs = NB * BS
+    torch.manual_seed(2)
+    flat = [torch.randn((NB, BS, H, D), device=DEV, dtype=torch.bfloat16) for _ in range(2 * L)]
+    ptrs = ptr_table(flat, DEV)
+    gen = torch.Generator().manual_seed(1)
+    blocks = torch.randperm(NB, generator=gen).tolist()
+    slots = torch.tensor(block_slots(blocks, BS, [1000, 1100, 996, 1000]), dtype=torch.int64, device=DEV)
+    starts = list(range(0, 4096, 256))
+    chunks = [torch.empty((2, L, 256, W), dtype=torch.bfloat16).pin_memory() for _ in starts]
+    ops.multi_layer_kv_transfer_batched(chunks, ptrs, slots, starts, torch.device(DEV), pbs, True, False, 2, W, W, 0)
+    _sync()
+    for c, s0 in zip(chunks, starts):
+        sl = slots[s0: s0 + 256]
+        want = torch.stack([torch.stack([flat[2 * l + p].reshape(-1, W).index_select(0, sl) for l in range(L)])
+                            for p in range(2)])
+        assert torch.equal(c.to(DEV).view(torch.int16), want.view(torch.int16))
+    checksum_before = [t.view(torch.int16).to(torch.int64).sum().item() for t in flat[:4]]
+    saved = [t.reshape(-1, W)[slots].clone() for t in flat]
+    for t in flat:
+        t.reshape(-1, W)[slots] = 0
+    ops.multi_layer_kv_transfer_batched(chunks, ptrs, slots, starts, torch.device(DEV), pbs, False, False, 2, W, W,
+                                        0)
+    _sync()
+    for t, s in zip(flat, saved):
+        assert torch.equal(t.reshape(-1, W)[slots].view(torch.int16), s.view(torch.int16))
+    checksum_after = [t.view(torch.int16).to(torch.int64).sum().item() for t in flat[:4]]
+    assert checksum_before == checksum_after
+    del flat, chunks, saved
+    torch.cuda.empty_cache()
+
+
 def test_binding_and_ctypes_paths_agree(ops):
     """The C++ binding and the ctypes calls reach the same library functions
     and move the same bytes."""

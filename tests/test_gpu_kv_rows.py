@@ -394,3 +394,120 @@ def test_fused_vs_oracle(ops, shape, fmt, slot_dtype):
     for f, w in zip(filled, want_t):
         assert np.array_equal(to_bytes(f), w)
     assert stg2.guards_intact()
+
+
+# ---------------------------------------------------------------------------
+# multi_layer_kv_transfer_batched over page-locked host memory objects
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_batched_pinned_vs_oracle(ops, fmt, slot_dtype):
+    """Five memory objects in page-locked host memory, one launch per
+    direction: the general row kernel with plain cache hints over several
+    objects, the launch the pinned-host benchmark mode times.  An empty
+    object sits mid-batch and a one-token object at the end.  Store: every
+    object equals the oracle's single-chunk result, guard bytes intact.
+    Retrieve: caches filled with the guard value end as the oracle's."""
+    gen = torch.Generator().manual_seed(40 + fmt)
+    L, NB, BS, W = 4, 64, 16, 1024
+    pbs = NB * BS
+    tens = _mk_planes(fmt, L, NB, BS, W, gen)
+    counts = [256, 0, 77, 100, 1]
+    starts = [0, 256, 256, 333, 433]
+    slots = _slots(pbs, 434, seed=50 + fmt, dtype=slot_dtype)
+    s64 = slots.numpy().astype(np.int64)
+    objs = [Guarded(2 * L * c * W * 2, device="cpu", pinned=True) for c in counts]
+    views = [o.view((2, L, c, W)) for o, c in zip(objs, counts)]
+    ops.multi_layer_kv_transfer_batched(views, ptr_table(tens, DEV), slots.to(DEV), starts, torch.device(DEV), pbs,
+                                        True, False, fmt, W, W, 0)
+    table_np = [to_bytes(t) for t in tens]
+    _sync()
+    for o, c, s in zip(objs, counts, starts):
+        want = np.full(2 * L * c * W * 2, GUARD, np.uint8)
+        ok.multi_layer_kv_transfer(want, table_np, s64[s: s + c], pbs, True, False, fmt, L, W, 2)
+        assert np.array_equal(o.bytes(), want)
+        assert o.guards_intact()
+    srcs = [randn_bf16((2, L, c, W), gen) for c in counts]
+    objs2 = [Guarded(2 * L * c * W * 2, device="cpu", pinned=True, fill=x) for x, c in zip(srcs, counts)]
+    views2 = [o.view((2, L, c, W)) for o, c in zip(objs2, counts)]
+    filled = [torch.full_like(t.view(torch.uint8), GUARD).view(torch.bfloat16) for t in tens]
+    ops.multi_layer_kv_transfer_batched(views2, ptr_table(filled, DEV), slots.to(DEV), starts, torch.device(DEV),
+                                        pbs, False, False, fmt, W, W, 0)
+    want_t = [np.full(t.numel() * 2, GUARD, np.uint8) for t in tens]
+    for x, c, s in zip(srcs, counts, starts):
+        ok.multi_layer_kv_transfer(to_bytes(x), want_t, s64[s: s + c], pbs, False, False, fmt, L, W, 2)
+    _sync()
+    for f, w in zip(filled, want_t):
+        assert np.array_equal(to_bytes(f), w)
+    for o, x in zip(objs2, srcs):
+        assert np.array_equal(o.bytes(), to_bytes(x)) and o.guards_intact()
+
+
+# ---------------------------------------------------------------------------
+# fused_multi_layer_kv_transfer for the MLA / DSA formats and use_mla
+# ---------------------------------------------------------------------------
+
+
+FUSED_FORMATS = {
+    # name: (format, use_mla, row widths of the planes each layer points to)
+    "mla_kv": (3, False, [512, 64]),
+    "dsa_kv": (4, False, [512, 64, 128]),
+    "mla_latent": (5, False, [512, 64]),
+    "dsa_index": (6, False, [128]),
+    "use_mla_merged": (1, True, [576]),
+    "use_mla_separate": (2, True, [576]),
+}
+
+
+@pytest.mark.parametrize("case", list(FUSED_FORMATS))
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_fused_formats_vs_oracle(ops, case, slot_dtype):
+    """The staged op sizes its staging copy per format
+    (csrc/mem_kernels.cpp:143-165): L * T * (kH + vH (+ dsaH)) elements for
+    the MLA / DSA formats, L * T * W for use_mla single-plane caches.  The
+    staging buffer is a sliced view inside a guarded buffer with room to
+    spare: store leaves the oracle's object in the host object and in the
+    first `required` staging bytes and nothing after them; load scatters the
+    host object into caches filled with the guard value."""
+    fmt, use_mla, widths = FUSED_FORMATS[case]
+    kH, vH, dsaH = (0, 0, 0) if use_mla else (512, 64, 128)
+    gen = torch.Generator().manual_seed(60 + fmt * 3 + use_mla)
+    L, NB, BS, T = 4, 64, 16, 300
+    pbs = NB * BS
+    wsum = sum(widths)
+    tens = [randn_bf16([NB, BS, 1, w], gen).to(DEV) for _ in range(L) for w in widths]
+    table_np = [to_bytes(t) for t in tens]
+    slots = _slots(pbs, T, seed=70 + fmt, dtype=slot_dtype)
+    s64 = slots.numpy().astype(np.int64)
+    required = L * T * wsum * 2
+    spare = L * 16 * wsum * 2
+    stg = Guarded(required + spare)
+    staging = stg.view((1, L, T + 16, wsum))[:, :, :T, :]
+    host = Guarded(required, device="cpu", pinned=True)
+    ops.fused_multi_layer_kv_transfer(host.view((1, L, T, wsum)), staging, ptr_table(tens, DEV), slots.to(DEV),
+                                      torch.device(DEV), pbs, True, use_mla, fmt, kH, vH, dsaH)
+    want = np.full(required, GUARD, np.uint8)
+    ok.multi_layer_kv_transfer(want, table_np, s64, pbs, True, use_mla, fmt, L, wsum, 2, kH, vH, dsaH)
+    _sync()
+    assert np.array_equal(host.bytes(), want)
+    assert host.guards_intact()
+    sb = stg.bytes()
+    assert np.array_equal(sb[:required], want)
+    assert (sb[required:] == GUARD).all()
+    assert stg.guards_intact()
+    src = randn_bf16((1, L, T, wsum), gen)
+    host2 = Guarded(required, device="cpu", pinned=True, fill=src)
+    filled = [torch.full_like(t.view(torch.uint8), GUARD).view(torch.bfloat16) for t in tens]
+    stg2 = Guarded(required + spare)
+    staging2 = stg2.view((1, L, T + 16, wsum))[:, :, :T, :]
+    ops.fused_multi_layer_kv_transfer(host2.view((1, L, T, wsum)), staging2, ptr_table(filled, DEV), slots.to(DEV),
+                                      torch.device(DEV), pbs, False, use_mla, fmt, kH, vH, dsaH)
+    want_t = [np.full(t.numel() * 2, GUARD, np.uint8) for t in tens]
+    ok.multi_layer_kv_transfer(to_bytes(src), want_t, s64, pbs, False, use_mla, fmt, L, wsum, 2, kH, vH, dsaH)
+    _sync()
+    for f, w in zip(filled, want_t):
+        assert np.array_equal(to_bytes(f), w)
+    assert np.array_equal(stg2.bytes()[:required], to_bytes(src))
+    assert stg2.guards_intact()
