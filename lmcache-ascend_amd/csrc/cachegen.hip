@@ -14,10 +14,14 @@
 //   L2  bases never decrease: an entry below its predecessor stands for
 //       0x10000, and entry n_bins is the end of the range (0x10000);
 //   L3  length = low bits, or 16 - floor(log2(width)) when they are 0;
-//   L4  calculate_cdf: Shannon lengths ceil(log2(n / count)) clamped to
-//       [1, 12], Kraft-repaired by lengthening the rarest present symbol,
-//       intervals assigned in symbol order with widths halved until aligned,
-//       absent symbols at the next present base;
+//   L4  calculate_cdf: the lengths of an optimal alphabetic code, the leaf
+//       depths of the Garsia-Wachs tree over the present symbols' counts
+//       (one present symbol: length 1), when the longest fits 8 bits (at
+//       most 256 counted symbols) or 12 (more); otherwise Shannon lengths
+//       ceil(log2(n / count)) clamped to [1, 12], Kraft-repaired by
+//       lengthening the rarest present symbol; intervals assigned in symbol
+//       order with widths halved until aligned (only ever needed for the
+//       Shannon lengths), absent symbols at the next present base;
 //   L5  encode writes at most `chunk` bytes per stream and reports the full
 //       byte length;
 //   L6  decode takes the largest symbol whose base is <= the next 16 bits.
@@ -31,6 +35,7 @@
 #include <type_traits>
 #include "common.h"
 #include "cachegen_decode.h"
+#include "cachegen_gw.h"
 #include "gmem.h"
 
 // Output words (CDF rows, bitstream words, decoded symbols) are stored with
@@ -102,111 +107,102 @@ __device__ __forceinline__ void unpack_row(const int16_t *row, int nb,
   }
 }
 
-__global__ void __launch_bounds__(kLanes)
-    cdf_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
-               int16_t *__restrict__ out, int tiles) {
-  extern __shared__ uint32_t lds[];
-  const int l = blockIdx.x / tiles;
-  const int c = (blockIdx.x % tiles) * kLanes + threadIdx.x;
-  if (c >= C) return;
-  uint32_t *col = lds + threadIdx.x;
-  for (int s = 0; s < nb; ++s) col[s * kLanes] = 0;
-  const uint8_t *p = in + static_cast<int64_t>(l) * T * C + c;
-  // kBatch symbol loads in flight per lane, then no-return LDS adds (each
-  // lane owns its histogram column, so there is no contention and no
-  // read-modify-write latency chain).
-  for (int t0 = 0; t0 < T; t0 += kBatch) {
-    uint32_t sym[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i)
-      sym[i] = t0 + i < T ? p[static_cast<int64_t>(t0 + i) * C] : 0xFFu;
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i)
-      if (sym[i] < static_cast<uint32_t>(nb)) atomicAdd(&col[sym[i] * kLanes], 1u);
-  }
-  // Code lengths (rule L4); entries become (count << 5) | length.
-  uint32_t n = 0;
-  for (int s = 0; s < nb; ++s) n += col[s * kLanes];
-  uint32_t kraft = 0;  // units of 2^-16; at most 64 * 2^15
-  for (int s = 0; s < nb; ++s) {
-    const uint32_t cnt = col[s * kLanes];
-    uint32_t len = 0;
-    if (cnt) {
-      while ((static_cast<uint64_t>(cnt) << len) < n) ++len;
-      len = len < 1 ? 1 : (len > kMaxLen ? kMaxLen : len);
-      kraft += 1u << (kPrec - len);
-    }
-    col[s * kLanes] = (cnt << 5) | len;
-  }
-  while (kraft > (1u << kPrec)) {
-    int pick = -1;
-    uint32_t best = 0;
-    for (int s = 0; s < nb; ++s) {
-      const uint32_t e = col[s * kLanes];
-      const uint32_t len = e & 31u;
-      if (len == 0 || len >= kMaxLen) continue;
-      if (pick < 0 || (e >> 5) <= best) {
-        pick = s;
-        best = e >> 5;
-      }
-    }
-    if (pick < 0) break;
-    const uint32_t e = col[pick * kLanes];
-    kraft -= 1u << (kPrec - (e & 31u) - 1);
-    col[pick * kLanes] = e + 1u;
-  }
-  // Aligned in-order assignment; entries become (base << 5) | length.
-  uint32_t pos = 0;
-  for (int s = 0; s < nb; ++s) {
-    uint32_t len = col[s * kLanes] & 31u;
-    if (len == 0) continue;
-    uint32_t w = 1u << (kPrec - len);
-    while (pos & (w - 1)) {
-      w >>= 1;
-      ++len;
-    }
-    col[s * kLanes] = (pos << 5) | len;
-    pos += w;
-  }
-  int16_t *o = out + (static_cast<int64_t>(l) * C + c) * (nb + 1);
-  uint32_t next = pos;
-  for (int s = nb - 1; s >= 0; --s) {
-    const uint32_t e = col[s * kLanes];
-    const uint32_t len = e & 31u;
-    uint32_t base;
-    if (len == 0) {
-      base = next;
-    } else {
-      base = e >> 5;
-      next = base;
-    }
-    o[s] = static_cast<int16_t>(static_cast<uint16_t>((base | len) & 0xFFFFu));
-  }
-  o[nb] = 0;
-}
-
-// Tiled calculate_cdf (1 <= T <= 256): 64 streams per block, four waves.
-// The block's symbols [T][64] are staged into LDS with 16-byte loads; wave
-// q counts the q-th quarter of the tokens into per-stream LDS histogram
-// columns (no-return adds, one column per lane); wave 0 then derives each
-// stream's CDF by rule L4, with closed forms for the Shannon length (the
-// smallest l with count << l >= n) and for the aligned width (the interval
-// width capped by the lowest set bit of the running base),
-// and the block's 64 rows, contiguous in the output, leave as coalesced
-// dword stores.  Rows equal the single-lane kernel's.
+// calculate_cdf: 64 streams per block, four waves.  The block's symbols are
+// staged into LDS 256 tokens at a time ([tokens][64] u8, 16-byte loads); wave
+// q counts the q-th quarter of each staged piece into per-stream LDS
+// histogram columns (no-return adds, one column per lane).  The derivation
+// is then spread over the waves: wave q takes symbols [j0, j1) of every
+// stream (lane = stream) for the count sums, the present-symbol counts, the
+// Shannon lengths of the fallback (the smallest l with count << l >= n, from
+// two leading-zero counts) and their Kraft sums.  The Garsia-Wachs lengths
+// (cachegen_gw.h) replace the Shannon ones of every stream whose tree fits
+// the length limit: one lane per stream in one wave when no stream of the
+// block has more than 16 present symbols, a quad of lanes per stream in all
+// four waves otherwise.  One wave, rotating with the block index so that the
+// blocks of a CU use different SIMDs, then makes the serial aligned
+// assignment (the width of each interval capped by the lowest set bit of the
+// running base), and the block's 64 rows, contiguous in the output, leave as
+// coalesced dword stores.
 constexpr int kCdfWaves = 4;
 constexpr int kCdfThreads = 64 * kCdfWaves;
-constexpr int kCdfMaxT = 256;
+constexpr int kCdfPiece = 256;  // tokens staged at a time
+// Histogram entries after the derivation: (length << kLenShift) | count.
+constexpr int kLenShift = 27;
+constexpr uint32_t kCountMask = (1u << kLenShift) - 1u;
 
-// kBins: register capacity for code lengths (nb <= kBins); kExact: nb ==
-// kBins, so every per-symbol bound is a constant.
+// Orders a wave's LDS writes before its later reads of other lanes' words
+// (a wave's LDS accesses are performed in order).
+__device__ __forceinline__ void wave_sync_cdf() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// LDS of cdf_tile_kernel: [staged symbols, later the compacted count lists]
+// [histogram [nb][64] u32] [count sums] [Kraft sums] [present symbols]
+// [rows [64][nb + 1] int16].
+__host__ __device__ constexpr int cdf_stage_words(int T, int nb) {
+  return ((T < kCdfPiece ? T : kCdfPiece) * 64 > nb * 256 ? ((T < kCdfPiece ? T : kCdfPiece) * 64 + 15) / 16 * 4
+                                                          : nb * 64);
+}
+__host__ __device__ constexpr int cdf_lds_bytes(int T, int nb) {
+  return 4 * (cdf_stage_words(T, nb) + nb * 64 + 3 * 64) + 64 * (nb + 1) * 2;
+}
+
+// Garsia-Wachs lengths for the streams of this lane's group (Q = 1: lane =
+// stream, one wave; Q = 4: four lanes per stream, 16 streams per wave).
+// Overwrites the stream's histogram entries with the tree's depths, and its
+// Kraft sum with 2^16 (a full code: nothing to repair), when the longest
+// depth fits the limit (8 bits for at most 256 counted symbols, else 12).
+template <int Q, int CAP, class It, int kBins>
+__device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint32_t *ksum, const uint32_t *nsum,
+                                           int nb, int stream, int g, int m_max) {
+  uint32_t *col = hist + stream;
+  uint32_t *lst = lists + stream;
+  // Compaction: the counts of the present symbols in symbol order.
+  uint64_t pres = 0;
+  int m = 0;
+  {
+    uint32_t cs[kBins];
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) cs[s] = s < nb ? col[s * 64] & kCountMask : 0u;
+#pragma unroll
+    for (int s = 0; s < kBins; ++s) {
+      if (s < nb && g == 0) lst[m * 64] = cs[s];
+      pres |= static_cast<uint64_t>(cs[s] != 0) << s;
+      m += cs[s] != 0 ? 1 : 0;
+    }
+  }
+  wave_sync_cdf();
+  typename It::V a[CAP];
+#pragma unroll
+  for (int i = 0; i < CAP; ++i) {
+    const int pos = Q * i + g;
+    const uint32_t w = lst[(pos < nb ? pos : nb - 1) * 64];
+    a[i] = pos < m ? It::leaf(w, pos) : It::inf();
+  }
+  cggw::Depths<typename It::L> dep;
+  cggw::run<Q, CAP, It>(a, g, m, m_max, dep);
+  const bool ok = m >= 2 && dep.over(nsum[stream] > 256u) == 0;
+  if (!ok) return;
+#pragma unroll
+  for (int s0 = 0; s0 < kBins; s0 += Q) {
+    const int s = s0 + g;
+    if (s < nb && ((pres >> s) & 1u)) {
+      const int j = __builtin_popcountll(pres & ((1ull << s) - 1ull));
+      col[s * 64] = (dep.depth(j) << kLenShift) | (col[s * 64] & kCountMask);
+    }
+  }
+  if (g == 0) ksum[stream] = 1u << kPrec;
+}
+
+// kBins: register capacity for per-symbol values (nb <= kBins); kExact: nb
+// == kBins, so every per-symbol bound is a constant.
 template <int kBins, bool kExact>
 __global__ void __launch_bounds__(kCdfThreads)
     cdf_tile_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
                     int16_t *__restrict__ out, int tiles, int vec_tile) {
   if (kExact) nb = kBins;
-  // [T][64] u8 symbols | [nb][64] u32 histogram | [64] u32 counts | [64] u32
-  // Kraft sums | [64][nb + 1] int16 rows
   extern __shared__ uint32_t lds[];
   const int tid = static_cast<int>(threadIdx.x);
   const int q = tid / 64;
@@ -215,75 +211,80 @@ __global__ void __launch_bounds__(kCdfThreads)
   const int c0 = (blockIdx.x % tiles) * 64;
   const int cnt = C - c0 < 64 ? C - c0 : 64;
   uint8_t *tile = reinterpret_cast<uint8_t *>(lds);
-  const int tile_words = (T * 64 + 15) / 16 * 4;
-  uint32_t *hist = lds + tile_words;
+  uint32_t *hist = lds + cdf_stage_words(T, nb);
   uint32_t *nsum = hist + nb * 64;   // per stream: symbol count
   uint32_t *ksum = nsum + 64;        // per stream: Kraft sum (units of 2^-16)
-  int16_t *rows = reinterpret_cast<int16_t *>(ksum + 64);
-  for (int i = tid; i < nb * 64 + 128; i += kCdfThreads) hist[i] = 0;
-  const uint8_t *src = in + static_cast<int64_t>(l) * T * C + c0;
-  const int pieces = T * 4;
-  if (vec_tile && cnt == 64) {
-    typedef unsigned int w4 __attribute__((ext_vector_type(4)));
-    w4 v[4];
-    int pi[4];
+  uint32_t *msum = ksum + 64;        // per stream: present symbols
+  int16_t *rows = reinterpret_cast<int16_t *>(msum + 64);
+  for (int i = tid; i < nb * 64 + 192; i += kCdfThreads) hist[i] = 0;
+  for (int t0 = 0; t0 < T; t0 += kCdfPiece) {
+    const int tc = T - t0 < kCdfPiece ? T - t0 : kCdfPiece;
+    if (t0 > 0) __syncthreads();  // the previous piece has been counted
+    const uint8_t *src = in + (static_cast<int64_t>(l) * T + t0) * C + c0;
+    const int pieces = tc * 4;
+    if (vec_tile && cnt == 64) {
+      typedef unsigned int w4 __attribute__((ext_vector_type(4)));
+      w4 v[4];
+      int pi[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = k * kCdfThreads + tid;
-      pi[k] = i < pieces ? i : pieces - 1;
-      v[k] = gload(reinterpret_cast<const w4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16));
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) reinterpret_cast<w4 *>(tile)[pi[k]] = v[k];
-  } else {
-    for (int i = tid; i < T * 64; i += kCdfThreads) {
-      const int c = i % 64;
-      tile[i] = c < cnt ? src[static_cast<int64_t>(i / 64) * C + c] : 0xFFu;
-    }
-  }
-  __syncthreads();
-  const int Tq = (T + kCdfWaves - 1) / kCdfWaves;
-  const int tb = q * Tq < T ? q * Tq : T;
-  const int te = tb + Tq < T ? tb + Tq : T;
-  if (lane < cnt && tb < te) {
-    // Symbols that are not counted add 0 to row 0 (no branch per symbol).
-    const int tq = te - tb;
-    const uint8_t *scol = tile + tb * 64 + lane;
-    for (int t0 = 0; t0 < tq; t0 += kBatch) {
-      uint32_t sym[kBatch];
-      if (t0 + kBatch <= tq) {
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) sym[i] = scol[(t0 + i) * 64];
-      } else {
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) sym[i] = t0 + i < tq ? scol[(t0 + i) * 64] : 0xFFu;
+      for (int k = 0; k < 4; ++k) {
+        const int i = k * kCdfThreads + tid;
+        pi[k] = i < pieces ? i : pieces - 1;
+        v[k] = gload(reinterpret_cast<const w4 *>(src + static_cast<int64_t>(pi[k] >> 2) * C + (pi[k] & 3) * 16));
       }
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const bool ok = sym[i] < static_cast<uint32_t>(nb);
-        atomicAdd(&hist[(ok ? sym[i] : 0u) * 64 + lane], ok ? 1u : 0u);
+      for (int k = 0; k < 4; ++k) reinterpret_cast<w4 *>(tile)[pi[k]] = v[k];
+    } else {
+      for (int i = tid; i < tc * 64; i += kCdfThreads) {
+        const int c = i % 64;
+        tile[i] = c < cnt ? src[static_cast<int64_t>(i / 64) * C + c] : 0xFFu;
+      }
+    }
+    __syncthreads();
+    const int Tq = (tc + kCdfWaves - 1) / kCdfWaves;
+    const int tb = q * Tq < tc ? q * Tq : tc;
+    const int te = tb + Tq < tc ? tb + Tq : tc;
+    if (lane < cnt && tb < te) {
+      // Symbols that are not counted add 0 to row 0 (no branch per symbol).
+      const int tq = te - tb;
+      const uint8_t *scol = tile + tb * 64 + lane;
+      for (int u0 = 0; u0 < tq; u0 += kBatch) {
+        uint32_t sym[kBatch];
+        if (u0 + kBatch <= tq) {
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) sym[i] = scol[(u0 + i) * 64];
+        } else {
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) sym[i] = u0 + i < tq ? scol[(u0 + i) * 64] : 0xFFu;
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const bool ok = sym[i] < static_cast<uint32_t>(nb);
+          atomicAdd(&hist[(ok ? sym[i] : 0u) * 64 + lane], ok ? 1u : 0u);
+        }
       }
     }
   }
   __syncthreads();
   // Derivation, spread over the waves: wave q takes symbols [j0, j1) of
-  // every stream (lane = stream) for the count sums, the code lengths and
-  // the Kraft sums; one wave per block, rotating with the block index so
-  // that the blocks of a CU use different SIMDs, then makes the serial
-  // aligned assignment.
+  // every stream (lane = stream).
   constexpr int kS = kBins / kCdfWaves;
   const int share = (nb + kCdfWaves - 1) / kCdfWaves;
   const int j0 = q * share;
   const int j1 = j0 + share < nb ? j0 + share : nb;
   uint32_t cnt_j[kS];
   {
-    uint32_t part = 0;
+    uint32_t part = 0, present = 0;
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       cnt_j[k] = (k < share && j0 + k < j1) ? hist[(j0 + k) * 64 + lane] : 0u;
       part += cnt_j[k];
+      present += cnt_j[k] != 0 ? 1u : 0u;
     }
-    if (lane < cnt && part) atomicAdd(nsum + lane, part);
+    if (lane < cnt && part) {
+      atomicAdd(nsum + lane, part);
+      atomicAdd(msum + lane, present);
+    }
   }
   __syncthreads();
   {
@@ -300,23 +301,47 @@ __global__ void __launch_bounds__(kCdfThreads)
         x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
         kpart += 1u << (kPrec - x);
       }
-      if (k < share && j0 + k < j1) hist[(j0 + k) * 64 + lane] = (x << 16) | cs;
+      if (k < share && j0 + k < j1) hist[(j0 + k) * 64 + lane] = (x << kLenShift) | cs;
     }
     if (lane < cnt && kpart) atomicAdd(ksum + lane, kpart);
   }
   __syncthreads();
+  // Garsia-Wachs lengths; the mode depends on the block's largest number of
+  // present symbols, the same in every wave.
+  {
+    uint32_t m_max = msum[lane];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m_max), d, 64));
+      m_max = o > m_max ? o : m_max;
+    }
+    const int mm = __builtin_amdgcn_readfirstlane(static_cast<int>(m_max));
+    uint32_t *lists = lds;  // the staged symbols are dead
+    if (mm >= 2) {
+      if (mm <= 16 && T < 65536) {
+        if (q == static_cast<int>(blockIdx.x % kCdfWaves))
+          gw_lengths<1, 16, cggw::Item16, kBins>(hist, lists, ksum, nsum, nb, lane, 0, mm);
+      } else if (mm <= 32) {
+        gw_lengths<4, 8, cggw::Item32, kBins>(hist, lists, ksum, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
+      } else if constexpr (kBins > 32) {
+        gw_lengths<4, 16, cggw::Item64, kBins>(hist, lists, ksum, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
+      }
+    }
+  }
+  __syncthreads();
   if (q == static_cast<int>(blockIdx.x % kCdfWaves) && lane < cnt) {
-    const uint32_t *col = hist + lane;  // (length << 16) | count
+    const uint32_t *col = hist + lane;  // (length << kLenShift) | count
     uint32_t len[kBins];
 #pragma unroll
     for (int s = 0; s < kBins; ++s) {
       const uint32_t v = col[(s < nb ? s : 0) * 64];  // every read issued before the first use
-      len[s] = s < nb ? v >> 16 : 0u;
+      len[s] = s < nb ? v >> kLenShift : 0u;
     }
-    // Kraft repair: lengthen the rarest present symbol below the cap (the
-    // last one among equals) until the code fits.  Never needed for T <=
-    // 256 (no Shannon length reaches the cap), so it runs out of line on
-    // the LDS copy of (length, count) and is kept out of the unrolled code.
+    // Kraft repair of the Shannon fallback: lengthen the rarest present
+    // symbol below the cap (the last one among equals) until the code fits.
+    // Needs a length capped at 12 bits (more than 4096 counted symbols), so
+    // it runs out of line on the LDS copy of (length, count) and is kept out
+    // of the unrolled code.
     uint32_t kraft = ksum[lane];
     if (kraft > (1u << kPrec)) {
       uint32_t *wcol = hist + lane;
@@ -325,24 +350,25 @@ __global__ void __launch_bounds__(kCdfThreads)
         uint32_t best = 0;
 #pragma unroll 1
         for (int s = 0; s < nb; ++s) {
-          const uint32_t v = wcol[s * 64], ls = v >> 16, cs = v & 0xFFFFu;
+          const uint32_t v = wcol[s * 64], ls = v >> kLenShift, cs = v & kCountMask;
           if (ls != 0 && ls < kMaxLen && (pick < 0 || cs <= best)) {
             pick = s;
             best = cs;
           }
         }
         if (pick < 0) break;
-        const uint32_t lp = wcol[pick * 64] >> 16;
+        const uint32_t lp = wcol[pick * 64] >> kLenShift;
         kraft -= 1u << (kPrec - lp - 1);
-        wcol[pick * 64] += 1u << 16;
+        wcol[pick * 64] += 1u << kLenShift;
       }
 #pragma unroll
-      for (int s = 0; s < kBins; ++s) len[s] = s < nb ? col[s * 64] >> 16 : 0u;
+      for (int s = 0; s < kBins; ++s) len[s] = s < nb ? col[s * 64] >> kLenShift : 0u;
     }
     // Aligned in-order assignment.  A symbol's base is the running position
     // `pos`, its width 2^(16 - length) capped by the lowest set bit of `pos`
-    // (the code lengthened to match); an absent symbol (length 0) gets the
-    // same value, which is the base of the next present symbol (or the end).
+    // (the code lengthened to match; never for the Garsia-Wachs lengths);
+    // an absent symbol (length 0) gets the same value, which is the base of
+    // the next present symbol (or the end).
     int16_t *row = rows + lane * (nb + 1);
     uint32_t pos = 0;
 #pragma unroll
@@ -1548,7 +1574,9 @@ __global__ void __launch_bounds__(kDecLanes)
   decode_one_wave<Tab>(lds, cdf, bytes, nbytes, prefix, T, C, nb, out, tiles, lane);
 }
 
+// Row-major contiguity; a tensor without elements has no layout to check.
 bool contiguous(const lmc_tensor &t) {
+  if (numel(t) == 0) return true;
   int64_t expect = 1;
   for (int i = t.ndim - 1; i >= 0; --i) {
     if (t.sizes[i] != 1 && t.strides[i] != expect) return false;
@@ -1589,28 +1617,17 @@ int lmc_calculate_cdf(const lmc_tensor *input, int32_t n_bins,
     check(T < (int64_t(1) << 26) && C < (int64_t(1) << 30), "input too large");
     if (L == 0 || C == 0) return;
     DeviceGuard guard(in.device);
-    if (T >= 1 && T <= kCdfMaxT) {
-      const int tiles64 = static_cast<int>((C + 63) / 64);
-      const size_t lds = 4 * (static_cast<size_t>((T * 64 + 15) / 16 * 4) + static_cast<size_t>(n_bins) * 64 + 128) +
-                         static_cast<size_t>(64) * (n_bins + 1) * 2;
-      const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
-      const auto kern = n_bins == 32         ? cdf_tile_kernel<32, true>
-                        : n_bins < 32          ? cdf_tile_kernel<32, false>
-                        : n_bins == kMaxBins   ? cdf_tile_kernel<kMaxBins, true>
-                                               : cdf_tile_kernel<kMaxBins, false>;
-      hipLaunchKernelGGL(kern, dim3(L * tiles64), dim3(kCdfThreads), lds, static_cast<hipStream_t>(stream),
-                         static_cast<const uint8_t *>(in.data), (int)T, (int)C, n_bins,
-                         static_cast<int16_t *>(o.data), tiles64, vec_tile);
-      hip_check(hipGetLastError(), "cdf_tile_kernel launch");
-      return;
-    }
-    const int tiles = static_cast<int>((C + kLanes - 1) / kLanes);
-    const size_t lds = static_cast<size_t>(n_bins) * kLanes * 4;
-    hipLaunchKernelGGL(cdf_kernel, dim3(L * tiles), dim3(kLanes), lds,
-                       static_cast<hipStream_t>(stream),
-                       static_cast<const uint8_t *>(in.data), (int)T, (int)C,
-                       n_bins, static_cast<int16_t *>(o.data), tiles);
-    hip_check(hipGetLastError(), "cdf_kernel launch");
+    const int tiles64 = static_cast<int>((C + 63) / 64);
+    const size_t lds = static_cast<size_t>(cdf_lds_bytes(static_cast<int>(T), n_bins));
+    const int vec_tile = (C % 16 == 0 && (reinterpret_cast<uintptr_t>(in.data) & 15) == 0) ? 1 : 0;
+    const auto kern = n_bins == 32         ? cdf_tile_kernel<32, true>
+                      : n_bins < 32          ? cdf_tile_kernel<32, false>
+                      : n_bins == kMaxBins   ? cdf_tile_kernel<kMaxBins, true>
+                                             : cdf_tile_kernel<kMaxBins, false>;
+    hipLaunchKernelGGL(kern, dim3(L * tiles64), dim3(kCdfThreads), lds, static_cast<hipStream_t>(stream),
+                       static_cast<const uint8_t *>(in.data), (int)T, (int)C, n_bins,
+                       static_cast<int16_t *>(o.data), tiles64, vec_tile);
+    hip_check(hipGetLastError(), "cdf_tile_kernel launch");
   });
 }
 

@@ -1,0 +1,252 @@
+// Code lengths of calculate_cdf's optimal alphabetic codes on the GPU.
+//
+// Rule L4 takes, for a stream with m >= 2 present symbols, the leaf depths
+// of the Garsia-Wachs combination tree over the present symbols' counts in
+// symbol order (A. M. Garsia and M. L. Wachs, "A new algorithm for minimum
+// cost binary trees", SIAM J. Comput. 6(4), 1977): while more than one item
+// is left, the first pair (x, y) of a triple x, y, z of consecutive weights
+// with x <= z, taken from the left (the last pair when no triple qualifies),
+// is combined and the combination re-inserted right after the nearest item
+// to its left whose weight is >= x + y (at the front when there is none).
+//
+// The list lives in registers.  An item packs its weight with the set of
+// leaves (present-symbol indices) below it, so that combining two items is
+// one addition (the leaf sets are disjoint); leaf depths are counted in
+// bit-sliced counters indexed by leaf.  A stream owns Q lanes (1, or a DPP
+// quad): list position q is slot q / Q of lane q % Q, so a combination step
+// costs each lane about 1/Q of the list, and the neighbours at q - 1, q + 1
+// and q + 2 arrive by quad permutations.  Positions past the list hold an
+// infinite weight, so every step processes a fixed number of slots; the
+// list shrinks by one per step and the slot count with it, in phases.
+#pragma once
+
+#include <stdint.h>
+
+namespace lmc {
+namespace cggw {
+
+// Up to 16 leaves and weights below 2^16: (weight << 16) | leaves.
+// kInf is the padding items' weight, above every real one.
+struct Item16 {
+  using V = uint32_t;
+  using L = uint32_t;
+  static constexpr uint32_t kInf = 0xFFFFu;
+  static __device__ __forceinline__ V leaf(uint32_t w, int j) { return (w << 16) | (1u << j); }
+  static __device__ __forceinline__ V inf() { return 0xFFFFFFFFu; }
+  static __device__ __forceinline__ uint32_t weight(V v) { return v >> 16; }
+  static __device__ __forceinline__ L leaves(V v) { return v & 0xFFFFu; }
+  static __device__ __forceinline__ V add(V a, V b) { return a + b; }
+  static __device__ __forceinline__ V zero() { return 0u; }
+  static __device__ __forceinline__ V bor(V a, V b) { return a | b; }
+};
+
+// Up to 32 leaves: (weight << 32) | leaves.
+struct Item32 {
+  using V = uint64_t;
+  using L = uint32_t;
+  static constexpr uint32_t kInf = 0xFFFFFFFFu;
+  static __device__ __forceinline__ V leaf(uint32_t w, int j) {
+    return (static_cast<uint64_t>(w) << 32) | (1u << j);
+  }
+  static __device__ __forceinline__ V inf() { return ~0ull; }
+  static __device__ __forceinline__ uint32_t weight(V v) { return static_cast<uint32_t>(v >> 32); }
+  static __device__ __forceinline__ L leaves(V v) { return static_cast<uint32_t>(v); }
+  static __device__ __forceinline__ V add(V a, V b) { return a + b; }
+  static __device__ __forceinline__ V zero() { return 0ull; }
+  static __device__ __forceinline__ V bor(V a, V b) { return a | b; }
+};
+
+// Up to 64 leaves: the leaf set and the weight side by side.
+struct Item64 {
+  struct V {
+    uint64_t m;
+    uint32_t w;
+  };
+  using L = uint64_t;
+  static constexpr uint32_t kInf = 0xFFFFFFFFu;
+  static __device__ __forceinline__ V leaf(uint32_t w, int j) { return V{1ull << j, w}; }
+  static __device__ __forceinline__ V inf() { return V{0ull, kInf}; }
+  static __device__ __forceinline__ uint32_t weight(V v) { return v.w; }
+  static __device__ __forceinline__ L leaves(V v) { return v.m; }
+  static __device__ __forceinline__ V add(V a, V b) { return V{a.m | b.m, a.w + b.w}; }
+  static __device__ __forceinline__ V zero() { return V{0ull, 0u}; }
+  static __device__ __forceinline__ V bor(V a, V b) { return V{a.m | b.m, a.w | b.w}; }
+};
+
+// Quad permutations: lane g of each group of four reads lane PERM[g].
+constexpr int kRot1 = 0x39;  // [1, 2, 3, 0]: the next lane
+constexpr int kRot2 = 0x4E;  // [2, 3, 0, 1]
+constexpr int kRot3 = 0x93;  // [3, 0, 1, 2]: the previous lane
+constexpr int kSwap = 0xB1;  // [1, 0, 3, 2]
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t qp(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t qp(uint64_t v) {
+  return (static_cast<uint64_t>(qp<CTRL>(static_cast<uint32_t>(v >> 32))) << 32) | qp<CTRL>(static_cast<uint32_t>(v));
+}
+template <int CTRL>
+__device__ __forceinline__ Item64::V qp(Item64::V v) {
+  return Item64::V{qp<CTRL>(v.m), qp<CTRL>(v.w)};
+}
+
+__device__ __forceinline__ uint32_t quad_min(uint32_t v) {
+  v = min(v, qp<kSwap>(v));
+  return min(v, qp<kRot2>(v));
+}
+__device__ __forceinline__ uint32_t quad_max(uint32_t v) {
+  v = max(v, qp<kSwap>(v));
+  return max(v, qp<kRot2>(v));
+}
+template <class It>
+__device__ __forceinline__ typename It::V quad_or(typename It::V v) {
+  v = It::bor(v, qp<kSwap>(v));
+  return It::bor(v, qp<kRot2>(v));
+}
+
+// Bit-sliced depth counters: bit j of d0..d3 is leaf j's depth (mod 16),
+// bit j of ovf is set once it reaches 16.
+template <class L>
+struct Depths {
+  L d0 = 0, d1 = 0, d2 = 0, d3 = 0, ovf = 0;
+  // One more level for every leaf in `mm`.
+  __device__ __forceinline__ void add(L mm) {
+    L c = d0 & mm;
+    d0 ^= mm;
+    L n = d1 & c;
+    d1 ^= c;
+    c = d2 & n;
+    d2 ^= n;
+    n = d3 & c;
+    d3 ^= c;
+    ovf |= n;
+  }
+  // Leaves deeper than 12 (wide) or 8 bits.
+  __device__ __forceinline__ L over(bool wide) const {
+    return (wide ? (d3 & d2 & (d1 | d0)) : (d3 & (d2 | d1 | d0))) | ovf;
+  }
+  __device__ __forceinline__ uint32_t depth(int j) const {
+    return static_cast<uint32_t>(((d0 >> j) & 1u) | (((d1 >> j) & 1u) << 1) | (((d2 >> j) & 1u) << 2) |
+                                 (((d3 >> j) & 1u) << 3));
+  }
+};
+
+// One combination step over a list of at most Q * S items (slots 0..S-1
+// of every lane; positions from Q * S on are padding).  g: the lane's place
+// in its stream's group; `active`: the stream still has two items or more.
+template <int Q, int S, int CAP, class It>
+__device__ __forceinline__ void step(typename It::V (&a)[CAP], int g, bool active,
+                                     Depths<typename It::L> &dep) {
+  using V = typename It::V;
+  static_assert(S <= CAP, "slots");
+  V up1[S], dn1[S];
+  uint32_t up2[S];
+  if constexpr (Q == 1) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      up1[i] = i + 1 < S ? a[i + 1 < S ? i + 1 : 0] : It::inf();
+      dn1[i] = i > 0 ? a[i > 0 ? i - 1 : 0] : It::inf();
+      up2[i] = i + 2 < S ? It::weight(a[i + 2 < S ? i + 2 : 0]) : It::kInf;
+    }
+  } else {
+    static_assert(Q == 4, "lanes per stream");
+    V r1[S], r3[S];
+    uint32_t r2[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      r1[i] = qp<kRot1>(a[i]);
+      r3[i] = qp<kRot3>(a[i]);
+      r2[i] = qp<kRot2>(It::weight(a[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const V next1 = i + 1 < S ? r1[i + 1 < S ? i + 1 : 0] : It::inf();
+      const V prev3 = i > 0 ? r3[i > 0 ? i - 1 : 0] : It::inf();
+      const uint32_t next2 = i + 1 < S ? r2[i + 1 < S ? i + 1 : 0] : It::kInf;
+      up1[i] = g == 3 ? next1 : r1[i];
+      dn1[i] = g == 0 ? prev3 : r3[i];
+      up2[i] = g >= 2 ? next2 : r2[i];
+    }
+  }
+  // The first position k whose triple qualifies, and the combined item.
+  int kslot = -1;
+  V sloc = It::zero();
+#pragma unroll
+  for (int i = S - 1; i >= 0; --i) {
+    const bool c = It::weight(a[i]) <= up2[i];
+    kslot = c ? i : kslot;
+    sloc = c ? It::add(a[i], up1[i]) : sloc;
+  }
+  int k;
+  V sum;
+  if constexpr (Q == 1) {
+    k = kslot;
+    sum = sloc;
+  } else {
+    const uint32_t kq = kslot >= 0 ? static_cast<uint32_t>(Q * kslot + g) : 0x3FFu;
+    k = static_cast<int>(quad_min(kq));
+    sum = quad_or<It>(kq == static_cast<uint32_t>(k) ? sloc : It::zero());
+  }
+  // Re-insertion point: right after the last position before k whose
+  // weight is >= the combined weight (0 when none is).
+  const uint32_t sw = It::weight(sum);
+  const int kg = k - g;
+  int pslot = -1;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const bool c = Q * i < kg && It::weight(a[i]) >= sw;
+    pslot = c ? i : pslot;
+  }
+  int p;
+  if constexpr (Q == 1) {
+    p = pslot + 1;
+  } else {
+    const uint32_t pq = pslot >= 0 ? static_cast<uint32_t>(Q * pslot + g + 1) : 0u;
+    p = static_cast<int>(quad_max(pq));
+  }
+  // New list: [0, p) kept, the combined item at p, (p, k] from one position
+  // to the left, the rest from one position to the right (k and k + 1 are
+  // gone).
+  const int pg = p - g;
+  V na[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    V v = Q * i <= kg ? dn1[i] : up1[i];
+    v = Q * i == pg ? sum : v;
+    na[i] = Q * i < pg ? a[i] : v;
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) a[i] = na[i];
+  dep.add(active ? It::leaves(sum) : typename It::L(0));
+}
+
+// Combination steps while the wave's longest list has more than Q * (S - 1)
+// items, then the phase with one slot fewer.  M: the wave's longest list
+// (wave-uniform); t: steps taken; m_lane: this stream's present symbols.
+template <int Q, int S, int CAP, class It>
+__device__ __forceinline__ void phases(typename It::V (&a)[CAP], int g, int m_lane, int &M, int &t,
+                                       Depths<typename It::L> &dep) {
+  if constexpr (S >= 1) {
+    while (M >= 2 && M > Q * (S - 1)) {
+      step<Q, S, CAP, It>(a, g, t < m_lane - 1, dep);
+      --M;
+      ++t;
+    }
+    phases<Q, S - 1, CAP, It>(a, g, m_lane, M, t, dep);
+  }
+}
+
+// Leaf depths of one stream's Garsia-Wachs tree, its first m_lane items in
+// a[] (the rest padding); m_max: the longest list of the wave, uniform.
+template <int Q, int CAP, class It>
+__device__ __forceinline__ void run(typename It::V (&a)[CAP], int g, int m_lane, int m_max,
+                                    Depths<typename It::L> &dep) {
+  int M = __builtin_amdgcn_readfirstlane(m_max);
+  int t = 0;
+  phases<Q, CAP, CAP, It>(a, g, m_lane, M, t, dep);
+}
+
+}  // namespace cggw
+}  // namespace lmc

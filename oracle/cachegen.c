@@ -32,13 +32,20 @@
  *       with w_s = base(s+1) - base(s); a symbol with w_s == 0 is absent and
  *       codes to nothing (as does a single symbol owning all of 0x10000).
  *   L4  calculate_cdf: counts c_s over the T tokens (symbols >= n_bins are
- *       not counted), n = sum of counts; l_s = clamp(ceil(log2(n / c_s)),
- *       1, 12) for present symbols; while the Kraft sum exceeds 1, lengthen
- *       the present symbol with l < 12 and the smallest count (ties: the
- *       highest symbol); then assign intervals in symbol order from 0, each
- *       at the running position, halving a symbol's width (lengthening its
- *       code) until the position is a multiple of it; absent symbols take the
- *       base of the next present symbol (or the end of the used range).
+ *       not counted), n = sum of counts, m present symbols (c_s > 0).
+ *       Lengths: one present symbol takes length 1.  For m >= 2 they are
+ *       the leaf depths of the Garsia-Wachs combination tree over the
+ *       present symbols' counts in symbol order, which are the lengths of an
+ *       optimal alphabetic (order-preserving) prefix code (oc_gw_lengths
+ *       states the tie rules), unless the longest exceeds Lmax = 8 when
+ *       n <= 256, else 12; those rows take the Shannon rule instead:
+ *       l_s = clamp(ceil(log2(n / c_s)), 1, 12), and while the Kraft sum
+ *       exceeds 1, lengthen the present symbol with l < 12 and the smallest
+ *       count (ties: the highest symbol).  Then assign intervals in symbol
+ *       order from 0, each at the running position, halving a symbol's width
+ *       (lengthening its code) until the position is a multiple of it (never
+ *       needed for the Garsia-Wachs lengths); absent symbols take the base
+ *       of the next present symbol (or the end of the used range).
  *   L5  encode writes at most `chunk` bytes per stream, leaves the rest of
  *       the row untouched and reports the full length in bytes; symbols
  *       >= n_bins code to nothing.
@@ -81,14 +88,110 @@ static void oc_unpack(const int16_t *row, int nb, uint32_t *u, int *len) {
   }
 }
 
+/* L4, optimal lengths: the leaf depths of the Garsia-Wachs combination tree
+ * over w[0..m-1] (m >= 2), written to depth[]; returns the largest.  The
+ * algorithm is A. M. Garsia and M. L. Wachs, "A new algorithm for minimum
+ * cost binary trees", SIAM J. Comput. 6(4), 1977 (also Knuth, TAOCP vol. 3,
+ * 6.2.2): while more than one weight is left, combine the first pair
+ * (x, y) of a triple x, y, z of consecutive weights with x <= z, taken from
+ * the left (the last pair when no triple qualifies, as if an infinite
+ * weight followed the list); remove both and re-insert x + y right after
+ * the nearest weight to the left of x's position that is >= x + y (at the
+ * front when there is none).  The tree's leaf depths are those of an
+ * optimal alphabetic tree over the weights in their order. */
+static int oc_gw_lengths(const uint64_t *w, int m, int *depth) {
+  uint64_t wt[2 * OC_MAX_BINS];
+  int parent[2 * OC_MAX_BINS];
+  int list[OC_MAX_BINS];
+  int len = m, next = m;
+  for (int i = 0; i < m; ++i) {
+    wt[i] = w[i];
+    list[i] = i;
+  }
+  while (len > 1) {
+    int k = len - 2;
+    for (int i = 0; i + 2 < len; ++i) {
+#ifdef OC_PLANT_GW_STRICT
+      /* planted mistake (tests only): the first triple with x < z */
+      if (wt[list[i]] < wt[list[i + 2]]) {
+#else
+      if (wt[list[i]] <= wt[list[i + 2]]) {
+#endif
+        k = i;
+        break;
+      }
+    }
+    const int a = list[k], b = list[k + 1];
+    const uint64_t sum = wt[a] + wt[b];
+    const int node = next++;
+    wt[node] = sum;
+    parent[a] = parent[b] = node;
+    for (int i = k; i + 2 < len; ++i) list[i] = list[i + 2];
+    len -= 2;
+    int p = 0;
+#ifdef OC_PLANT_GW_IN_PLACE
+    /* planted mistake (tests only): the combined weight stays at x's place */
+    p = k;
+#else
+    for (int j = k - 1; j >= 0; --j)
+      if (wt[list[j]] >= sum) {
+#ifdef OC_PLANT_GW_BEFORE
+        /* planted mistake (tests only): re-inserted before that weight */
+        p = j;
+#else
+        p = j + 1;
+#endif
+        break;
+      }
+#endif
+    for (int i = len; i > p; --i) list[i] = list[i - 1];
+    list[p] = node;
+    ++len;
+  }
+  /* Parents are created after their children: depths from the root down. */
+  int d[2 * OC_MAX_BINS];
+  d[next - 1] = 0;
+  for (int id = next - 2; id >= 0; --id) d[id] = d[parent[id]] + 1;
+  int longest = 0;
+  for (int i = 0; i < m; ++i) {
+    depth[i] = d[i];
+    if (d[i] > longest) longest = d[i];
+  }
+  return longest;
+}
+
 /* L4 for one stream: counts -> int16 row of nb + 1 entries. */
 static void oc_cdf_row(const uint32_t *count, int nb, int16_t *row) {
   uint64_t n = 0;
   for (int s = 0; s < nb; ++s) n += count[s];
   int len[OC_MAX_BINS];
   uint32_t base[OC_MAX_BINS];
-  uint64_t kraft = 0; /* in units of 2^-16 */
+  uint64_t w[OC_MAX_BINS];
+  int sym[OC_MAX_BINS], depth[OC_MAX_BINS];
+  int m = 0;
   for (int s = 0; s < nb; ++s) {
+    len[s] = 0;
+    if (count[s]) {
+      w[m] = count[s];
+      sym[m++] = s;
+    }
+  }
+#ifdef OC_PLANT_LMAX9
+  /* planted mistake (tests only): a 9-bit limit for short chunks */
+  const int lmax = n <= 256 ? 9 : OC_MAX_LEN;
+#else
+  const int lmax = n <= 256 ? 8 : OC_MAX_LEN;
+#endif
+  int optimal = 0;
+  if (m == 1) {
+    len[sym[0]] = 1;
+    optimal = 1;
+  } else if (m >= 2 && oc_gw_lengths(w, m, depth) <= lmax) {
+    for (int i = 0; i < m; ++i) len[sym[i]] = depth[i];
+    optimal = 1;
+  }
+  uint64_t kraft = 0; /* in units of 2^-16 */
+  for (int s = 0; s < nb && !optimal; ++s) {
     if (count[s] == 0) {
       len[s] = 0;
       continue;
@@ -104,7 +207,7 @@ static void oc_cdf_row(const uint32_t *count, int nb, int16_t *row) {
     len[s] = l;
     kraft += (uint64_t)1 << (OC_PREC - l);
   }
-  while (kraft > ((uint64_t)1 << OC_PREC)) {
+  while (!optimal && kraft > ((uint64_t)1 << OC_PREC)) {
     int pick = -1;
     for (int s = 0; s < nb; ++s) {
       if (len[s] == 0 || len[s] >= OC_MAX_LEN) continue;
@@ -122,13 +225,19 @@ static void oc_cdf_row(const uint32_t *count, int nb, int16_t *row) {
   uint32_t pos = 0;
   for (int s = 0; s < nb; ++s) {
     if (len[s] == 0) continue;
-    uint32_t w = 1u << (OC_PREC - len[s]);
-    while (pos & (w - 1)) {
-      w >>= 1;
+    uint32_t wd = 1u << (OC_PREC - len[s]);
+#ifdef OC_PLANT_ROUND_UP
+    /* planted mistake (tests only): the base is rounded up to the width and
+     * the length kept, instead of the width halved */
+    pos = (pos + wd - 1) & ~(wd - 1);
+#else
+    while (pos & (wd - 1)) {
+      wd >>= 1;
       ++len[s];
     }
+#endif
     base[s] = pos;
-    pos += w;
+    pos += wd;
   }
   uint32_t next = pos;
   for (int s = nb - 1; s >= 0; --s) {

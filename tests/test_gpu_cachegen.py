@@ -351,11 +351,12 @@ def test_codec_through_ctypes(ops, monkeypatch):
     assert torch.equal(dec, d)
 
 
-@pytest.mark.parametrize("T,C,nb", [(256, 1024, 32), (100, 100, 17), (300, 70, 32), (1, 64, 64)])
+@pytest.mark.parametrize("T,C,nb", [(256, 1024, 32), (100, 100, 17), (300, 70, 32), (1, 64, 64), (0, 64, 32)])
 def test_calculate_cdf_writes_every_entry(ops, T, C, nb):
     """calculate_cdf allocates its output without a fill: the kernels must
     write every entry.  Called through the C ABI into an output holding
-    -1 everywhere (tiled kernel for T <= 256, one lane per stream above)."""
+    -1 everywhere (tiled kernel for 1 <= T <= 256, one lane per stream
+    above and for T = 0, where every row is zeros: no symbol is present)."""
     rng = np.random.default_rng(T + C + nb)
     syms = rng.integers(0, nb, size=(3, T, C), dtype=np.uint8)
     d = torch.from_numpy(syms).to(DEV)
@@ -364,3 +365,93 @@ def test_calculate_cdf_writes_every_entry(ops, T, C, nb):
     ops._run(ops._L.lmc_calculate_cdf(ops._ref(a), nb, ops._ref(o), ops._stream(0)))
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), oc.calculate_cdf(syms, nb))
+
+
+@pytest.mark.parametrize("C", [128, 96])
+def test_decode_empty_streams_write_every_symbol(ops, C):
+    """decode's output is allocated without a fill by decode_chunk: with
+    every stream empty (all lengths 0), decode still writes every symbol
+    (bits past a stream's end read as zeros, rule L6) into an output that
+    holds 0xEE.  C = 128 is two full 64-stream blocks (per-lane regions),
+    C = 96 adds a partial block (the shared-window path)."""
+    rng = np.random.default_rng(77 + C)
+    L, T, nb = 2, 40, 32
+    syms = rng.integers(0, nb, size=(L, T, C), dtype=np.uint8)
+    cdf = oc.calculate_cdf(syms, nb)
+    stream = np.zeros(64, np.uint8)
+    pref = np.zeros((L, C), np.int32)
+    out = torch.full((L, T, C), 0xEE, dtype=torch.uint8, device=DEV)
+    ops.decode_fast_prefsum(torch.from_numpy(cdf).to(DEV), torch.from_numpy(stream).to(DEV),
+                            torch.from_numpy(pref).to(DEV), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), oc.decode(cdf, stream, pref, T))
+
+
+FIB = [1, 1, 2, 3, 5, 8, 13, 21, 34, 55, 89]
+
+
+def _channels_from_counts(rng, counts_per_channel, T, nb):
+    """[T, C] symbols: channel c holds counts[c][s] copies of symbol s in a
+    random order, the rest of its T tokens out of range (not counted)."""
+    C = len(counts_per_channel)
+    out = np.full((T, C), nb + 1, np.uint8)
+    for c, counts in enumerate(counts_per_channel):
+        col = np.repeat(np.arange(len(counts), dtype=np.uint8), counts)
+        assert col.size <= T
+        out[: col.size, c] = col
+        out[:, c] = rng.permutation(out[:, c])
+    return out
+
+
+def _gaussian_counts(rng, T, bins, nb):
+    x = rng.normal(size=(T, 1)).astype(np.float32)
+    q = oc.quantize(x[None], bins)[0, :, 0]
+    return np.bincount(q, minlength=nb)[:nb].tolist()
+
+
+def _fib_counts(rng, nb, extra):
+    """A Fibonacci run (a Garsia-Wachs tree deeper than 8 levels within 256
+    symbols) beside `extra` rare symbols, forwards or backwards."""
+    tail = [int(x) for x in rng.integers(1, 3, size=extra)] + [0] * (nb - len(FIB) - extra)
+    c = FIB + tail
+    return c if rng.random() < 0.5 else c[::-1]
+
+
+@pytest.mark.parametrize("case", ["one_lane", "quad32", "quad64", "quad64_not_exact", "fallback_one_lane",
+                                  "fallback_quad", "long_few_counted", "long_wide_items"])
+def test_calculate_cdf_modes_vs_oracle(ops, case):
+    """calculate_cdf picks, per block of 64 streams, one lane per stream
+    (at most 16 present symbols) or a quad of lanes per stream with 32- or
+    64-leaf items; each mode, rows that fall back to the Shannon lengths
+    (Garsia-Wachs trees deeper than 8 levels), chunks longer than 256
+    tokens with at most 256 counted symbols (8-bit limit) and chunks of
+    65536 tokens or more (no 16-bit items) are bit-exact against the
+    oracle."""
+    rng = np.random.default_rng(sum(map(ord, case)))
+    T, nb, C = 256, 32, 128
+    if case == "one_lane":
+        rows = [_gaussian_counts(rng, T, 16, nb) for _ in range(C)]
+    elif case == "quad32":
+        rows = [_gaussian_counts(rng, T, 32, nb) for _ in range(C)]
+    elif case in ("quad64", "quad64_not_exact"):
+        nb = 64 if case == "quad64" else 50
+        rows = [_gaussian_counts(rng, T, 64 if nb == 64 else 50, nb) for _ in range(C)]
+    elif case == "fallback_one_lane":
+        rows = [_fib_counts(rng, nb, int(rng.integers(0, 5))) if c % 3 == 0 else _gaussian_counts(rng, T, 16, nb)
+                for c in range(C)]
+    elif case == "fallback_quad":
+        rows = [_fib_counts(rng, nb, int(rng.integers(5, 15))) if c % 3 == 0 else _gaussian_counts(rng, T, 32, nb)
+                for c in range(C)]
+    elif case == "long_few_counted":
+        T = 700
+        rows = [_gaussian_counts(rng, 200, 16 if c < 64 else 32, nb) for c in range(C)]
+    else:
+        T, C = 65536, 64
+        rows = [[4096] * 16 + [0] * 16 for _ in range(C)]
+        rows[5] = [32769] + [2 ** j for j in range(15)] + [0] * 16  # a 15-level caterpillar: fallback
+    syms = _channels_from_counts(rng, rows, T, nb)[None]
+    d = torch.from_numpy(syms).to(DEV)
+    cdf = ops.calculate_cdf(d, nb)
+    want = oc.calculate_cdf(syms, nb)
+    torch.cuda.synchronize()
+    assert np.array_equal(cdf.cpu().numpy(), want)
