@@ -79,9 +79,11 @@ constexpr int kRot2 = 0x4E;  // [2, 3, 0, 1]
 constexpr int kRot3 = 0x93;  // [3, 0, 1, 2]: the previous lane
 constexpr int kSwap = 0xB1;  // [1, 0, 3, 2]
 
+// Every lane of a quad is a valid source, so no value for invalid lanes is
+// needed (bound_ctrl set: no old value tied to the destination).
 template <int CTRL>
 __device__ __forceinline__ uint32_t qp(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ uint64_t qp(uint64_t v) {
