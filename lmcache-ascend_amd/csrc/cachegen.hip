@@ -1650,8 +1650,7 @@ int lmc_encode_fast_new(const lmc_tensor *cdf_t, const lmc_tensor *input_sym,
     const int64_t chunk = ob.sizes[2];
     // csrc/cachegen_kernels.cpp:33-35
     check(C <= (1 << 15),
-          "Number of channels exceeds that supported be encode, contact "
-          "LMCache Ascend about changing this limitation");
+          "encode takes at most 32768 channels per layer");
     check(in.dtype == LMC_U8 || in.dtype == LMC_I8, "input_sym must be int8/uint8");
     check(cdf.dtype == LMC_I16, "cdf must be int16");
     check(ob.dtype == LMC_U8 || ob.dtype == LMC_I8, "output_buffer must be uint8");
@@ -1746,11 +1745,8 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf_t,
     need_device(o, "output");
     check(cdf.ndim == 3, "cdf must be [L, C, nbins + 1]");
     const int64_t L = cdf.sizes[0], C = cdf.sizes[1], nb = cdf.sizes[2] - 1;
-    check(C % 32 == 0,
-          "Decode implementation relies on the number of channels being a "
-          "multiple of 32, contact LMCache Ascend about changing this "
-          "limitation");
-    check(nb < 64, "Max bins constraint violated");
+    check(C % 32 == 0, "decode takes a channel count that is a multiple of 32");
+    check(nb < 64, "decode takes fewer than 64 bins per stream");
     check(nb >= 1, "cdf needs at least one bin");
     check(cdf.dtype == LMC_I16, "cdf must be int16");
     check(bs.dtype == LMC_U8 || bs.dtype == LMC_I8, "bytestreams must be uint8");

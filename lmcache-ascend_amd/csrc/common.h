@@ -129,15 +129,15 @@ uintptr_t translate_host_ptr(uintptr_t host, size_t required);
 
 // Kernel-visible address of a tensor: device tensors pass through, host
 // tensors must be pinned and mapped (the reference's get_kernel_ptr,
-// csrc/utils.h:32-51, and its error text).
+// csrc/utils.h:32-51).
 inline uint8_t *kernel_ptr(const lmc_tensor &t) {
   if (t.device >= 0) return static_cast<uint8_t *>(t.data);
   uintptr_t dev = translate_host_ptr(reinterpret_cast<uintptr_t>(t.data),
                                      static_cast<size_t>(
                                          extent_bytes(t) > 0 ? extent_bytes(t) : 1));
   if (dev == 0)
-    fail(LMC_ERR_RUNTIME, "Unable to retrieve device ptr, is this a host "
-                          "registered pointer ?");
+    fail(LMC_ERR_RUNTIME, "host tensor is not in pinned, device-mapped memory: "
+                          "no device address for it");
   return reinterpret_cast<uint8_t *>(dev);
 }
 

@@ -101,7 +101,7 @@ void submit_1d(const Seg &s, hipMemcpyKind kind, hipStream_t stream) {
   hipError_t e = hipMemcpyAsync(reinterpret_cast<void *>(s.dst), reinterpret_cast<const void *>(s.src),
                                 s.bytes, kind, stream);
   if (e != hipSuccess)
-    fail(LMC_ERR_RUNTIME, std::string("Layerwise prefill DMA submission failed: ret=") +
+    fail(LMC_ERR_RUNTIME, std::string("layerwise prefill copies were not enqueued: status ") +
                               std::to_string(static_cast<int>(e)) + " bytes=" + std::to_string(s.bytes) +
                               " (" + hipGetErrorString(e) + ")");
 }
@@ -278,7 +278,7 @@ void dma_copy_diagnose(const lmc_dma_segment *rows, int64_t n, bool d2h, hipStre
                                   reinterpret_cast<const void *>(rows[i].src), rows[i].bytes, kind, stream);
     copy_us[i] = std::chrono::duration<double, std::micro>(Clock::now() - t0).count();
     if (e != hipSuccess)
-      fail(LMC_ERR_RUNTIME, std::string("Diagnostic DMA submission failed: ret=") +
+      fail(LMC_ERR_RUNTIME, std::string("diagnostic copies were not enqueued: status ") +
                                 std::to_string(static_cast<int>(e)) + " segment=" + std::to_string(i) +
                                 " bytes=" + std::to_string(rows[i].bytes));
   }

@@ -145,7 +145,7 @@ uintptr_t create(size_t size, const std::string &name, const std::vector<int> &n
 uintptr_t attach(size_t size, const std::string &name, bool writable) {
   check_size_and_name("attach_shm_pinned_ptr", size, name);
   const int fd = shm_open(name.c_str(), writable ? O_RDWR : O_RDONLY, 0600);
-  if (fd < 0) fail(LMC_ERR_RUNTIME, "shm_open attach failed for " + name + ": " + why(errno));
+  if (fd < 0) fail(LMC_ERR_RUNTIME, "cannot open shared-memory segment " + name + ": " + why(errno));
   struct FdCloser {
     int fd;
     ~FdCloser() { close(fd); }

@@ -204,7 +204,9 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
   }
 }
 
-// IndexerC8State's checks (csrc/indexer_c8.cpp:13-50), with its messages.
+// IndexerC8State's conditions (csrc/indexer_c8.cpp:13-50).  Two messages keep
+// the phrases the reference's test matches ("float16 scales", "int32/int64
+// vectors": tests/standalone/test_indexer_c8_native.py:100,104).
 void check_state(const lmc_tensor &keys, const lmc_tensor *scales,
                  int64_t factor, const lmc_tensor *block_map) {
   check(keys.device >= 0 && (scales == nullptr || scales->device == keys.device),
@@ -212,7 +214,7 @@ void check_state(const lmc_tensor &keys, const lmc_tensor *scales,
   const bool quantized = keys.dtype == LMC_I8;
   check(quantized ? scales != nullptr && scales->dtype == LMC_F16
                   : scales == nullptr && (keys.dtype == LMC_F16 || keys.dtype == LMC_BF16),
-        "Indexer requires floating keys alone, or int8 keys and float16 scales");
+        "indexer caches: float16/bfloat16 keys without scales, or int8 keys with float16 scales");
   auto contiguous = [](const lmc_tensor &t) {
     int64_t expect = 1;
     for (int i = t.ndim - 1; i >= 0; --i) {
@@ -223,19 +225,19 @@ void check_state(const lmc_tensor &keys, const lmc_tensor *scales,
   };
   check(keys.ndim == 4 && keys.sizes[0] > 0 && keys.sizes[1] == 128 && keys.sizes[2] == 1 &&
             keys.sizes[3] == 128 && contiguous(keys),
-        "Indexer destinations require contiguous PA_BSND storage");
+        "indexer keys are not a contiguous [blocks, 128, 1, 128] cache");
   check((factor == 1 || (factor == 2 && quantized)) && keys.sizes[0] % factor == 0,
-        "Invalid physical indexer block factor");
+        "indexer block factor is neither 1 nor 2 (int8 keys), or does not divide the blocks");
   check(!quantized || (scales->ndim == 4 && scales->sizes[0] == keys.sizes[0] &&
                        scales->sizes[1] == 128 && scales->sizes[2] == 1 &&
                        scales->sizes[3] == 1 && contiguous(*scales)),
-        "C8 destinations require paired contiguous PA_BSND storage");
+        "C8 scales are not a contiguous [blocks, 128, 1, 1] cache beside the keys");
   check(block_map == nullptr ||
             (quantized && factor == 1 && block_map->device == keys.device &&
              block_map->dtype == LMC_I32 && block_map->ndim == 1 &&
              block_map->sizes[0] == keys.sizes[0] && contiguous(*block_map)),
-        "C8 block permutation must be a complete contiguous int32 vector on the "
-        "cache device");
+        "C8 block map: one contiguous int32 entry per block, on the keys' GPU, "
+        "for int8 keys at factor 1");
 }
 
 int64_t cache_slots_of(const lmc_tensor &keys, int64_t factor) {
@@ -245,7 +247,7 @@ int64_t cache_slots_of(const lmc_tensor &keys, int64_t factor) {
 void check_vector(const lmc_tensor &t, int device) {
   check(t.device == device && (t.dtype == LMC_I64 || t.dtype == LMC_I32) && t.ndim == 1 &&
             (t.sizes[0] <= 1 || t.strides[0] == 1),
-        "C8 copy metadata must be contiguous int32/int64 vectors on the cache device");
+        "C8 slots, offsets and counts: int32/int64 vectors, contiguous, on the keys' GPU");
 }
 
 void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
@@ -253,7 +255,7 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
                  const lmc_tensor &ptrs, const lmc_tensor &offs, const lmc_tensor &counts,
                  const lmc_tensor &slots, int64_t capacity, bool from_npu, bool fixed,
                  hipStream_t stream) {
-  check(n_layers > 0 && keys && factors, "C8 group must contain at least one layer");
+  check(n_layers > 0 && keys && factors, "C8 group holds no layer");
   C8Job job;
   std::memset(&job, 0, sizeof(job));
   const lmc_tensor &k0 = deref(keys[0], "keys");
@@ -266,16 +268,16 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
     check_state(k, s, factors[l], m);
     const int64_t cs = cache_slots_of(k, factors[l]);
     check(k.device == dev && (cache_slots < 0 || cs == cache_slots),
-          "C8 group layers must share device and slot capacity");
+          "C8 group layers differ in GPU or in slot capacity");
     cache_slots = cs;
   }
   // csrc/indexer_c8.cpp:65-95 (a group's pointers are [layers, chunks]).
   if (n_layers > 1 || ptrs.ndim == 2) {
     check(ptrs.ndim == 2 && ptrs.sizes[0] == n_layers &&
               (ptrs.sizes[1] <= 1 || (ptrs.strides[1] == 1 && ptrs.strides[0] == ptrs.sizes[1])),
-          "C8 group pointers must have shape [layers, chunks]");
+          "C8 group packet pointers are not a contiguous [layers, chunks] table");
     check(ptrs.device == dev && ptrs.dtype == LMC_I64,
-          "C8 copy metadata must be contiguous int32/int64 vectors on the cache device");
+          "C8 slots, offsets and counts: int32/int64 vectors, contiguous, on the keys' GPU");
   } else {
     check_vector(ptrs, dev);
   }
@@ -283,15 +285,15 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
   check_vector(counts, dev);
   check_vector(slots, dev);
   check(ptrs.dtype == LMC_I64 && offs.dtype == counts.dtype,
-        "C8 pointers must be int64; offsets and counts must share a dtype");
+        "C8 packet pointers are not int64, or offsets and counts differ in dtype");
   const int64_t chunks = ptrs.ndim == 2 ? ptrs.sizes[1] : ptrs.sizes[0];
   check(fixed || (numel(offs) == chunks && numel(counts) == chunks),
-        "C8 pointer, offset and count vectors must have equal lengths");
-  check(capacity > 0 && capacity <= INT32_MAX, "C8 chunk capacity is out of range");
+        "C8 packet pointers, offsets and counts differ in length");
+  check(capacity > 0 && capacity <= INT32_MAX, "C8 chunk capacity is not in [1, 2^31)");
   if (chunks == 0) return;
   const int64_t slot_count = numel(slots);
   check(!fixed || (slot_count + capacity - 1) / capacity == chunks,
-        "C8 fixed chunks do not cover the slot mapping");
+        "C8 fixed-capacity chunks and the slot mapping differ in token count");
   check(chunks <= 65535, "C8 transfer has more chunks than one launch grid holds");
   DeviceGuard guard(dev);
   job.offsets = offs.data;
@@ -308,7 +310,7 @@ void c8_transfer(const lmc_tensor *const *keys, const lmc_tensor *const *scales,
   const int64_t tile_tokens = from_npu ? kC8Threads / kPackGroup * kPackUnroll
                                       : kC8Threads / kUnpackGroup * kUnpackUnroll;
   const int64_t tiles = (capacity + tile_tokens - 1) / tile_tokens;
-  check(tiles < (int64_t(1) << 31), "C8 transfer grid is too large");
+  check(tiles < (int64_t(1) << 31), "C8 chunk capacity needs more tiles than one launch holds");
   for (int l0 = 0; l0 < n_layers; l0 += kC8Layers) {
     const int nl = std::min(kC8Layers, n_layers - l0);
     C8Job j = job;

@@ -486,25 +486,26 @@ const lmc_tensor &index_tensor(const lmc_tensor *t, const char *name) {
   return x;
 }
 
-// csrc/utils.cpp:968-998, with the reference's messages.
+// The input conditions of csrc/utils.cpp:968-998 (messages in this library's
+// words).
 void validate_sparse_inputs(const lmc_tensor &slots, const lmc_tensor &sel) {
   if ((slots.ndim != 1 && slots.ndim != 2) || slots.ndim != sel.ndim)
-    fail(LMC_ERR_VALUE, "slot_mapping_packed and selected_token_idx must both "
-                        "be 1D or both be 2D.");
+    fail(LMC_ERR_VALUE, "slot_mapping_packed and selected_token_idx: one is 1-D "
+                        "and the other 2-D, or neither is 1-D or 2-D");
   for (int i = 0; i < slots.ndim; ++i)
     if (slots.sizes[i] != sel.sizes[i])
-      fail(LMC_ERR_VALUE, "slot_mapping_packed and selected_token_idx must "
-                          "have the same length.");
+      fail(LMC_ERR_VALUE, "slot_mapping_packed and selected_token_idx differ "
+                          "in shape");
   if (sel.dtype != LMC_I32)
-    fail(LMC_ERR_VALUE, "selected_token_idx must be torch.int32.");
+    fail(LMC_ERR_VALUE, "selected_token_idx holds int32 token indices");
   if (sel.device < 0)
-    fail(LMC_ERR_VALUE, "selected_token_idx must be on the GPU.");
+    fail(LMC_ERR_VALUE, "selected_token_idx is not a GPU tensor");
 }
 
 void set_sparse_indices(EntryJob &job, const lmc_tensor &slots,
                         const lmc_tensor &sel) {
   check(numel(slots) == numel(sel),
-        "slot_mapping_packed and selected_token_idx must have the same length.");
+        "slot_mapping_packed and selected_token_idx differ in length");
   job.slots = kernel_ptr(slots);
   job.slot_i32 = slots.dtype == LMC_I32;
   job.tokens = kernel_ptr(sel);
@@ -533,9 +534,9 @@ void sparse_single_layer(const lmc_tensor *lmc_t, const lmc_tensor *caches,
 
 const lmc_tensor &chunk_table(const lmc_tensor *t) {
   const lmc_tensor &x = deref(t, "chunk_ptrs_npu");
-  check(x.dtype == LMC_I64, "chunk_ptrs_npu must be torch.int64.");
-  check(x.device >= 0, "chunk_ptrs_npu must be on the GPU.");
-  check(numel(x) > 0, "chunk_ptrs_npu must not be empty.");
+  check(x.dtype == LMC_I64, "chunk_ptrs_npu holds int64 addresses");
+  check(x.device >= 0, "chunk_ptrs_npu is not a GPU tensor");
+  check(numel(x) > 0, "chunk_ptrs_npu lists no chunk");
   check(x.ndim == 1 && (x.sizes[0] <= 1 || x.strides[0] == 1),
         "chunk_ptrs_npu must be a contiguous 1-D table");
   check(numel(x) < (int64_t(1) << 31), "too many chunks");
@@ -554,8 +555,8 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   const lmc_tensor &sel = index_tensor(sel_t, "selected_token_idx");
   if (validate) validate_sparse_inputs(slots, sel);
   // csrc/mem_kernels.cpp:601-602, 692-693.
-  check(chunk_size > 0, "chunk_size must be positive.");
-  check(total_tokens > 0, "total_tokens must be positive.");
+  check(chunk_size > 0, "chunk_size is not positive");
+  check(total_tokens > 0, "total_tokens is not positive");
   check(chunk_size < (int64_t(1) << 31) && total_tokens < (int64_t(1) << 31),
         "chunk_size and total_tokens must fit int32");
   const lmc_tensor &ptrs = chunk_table(ptrs_t);
@@ -597,34 +598,35 @@ void sparse_direct(const lmc_tensor *ptrs_t, const lmc_tensor *sample_t,
   launch_entries(job, true, stream);
 }
 
-// csrc/mem_kernels.cpp:978-1034, with the reference's messages.
+// The input conditions of csrc/mem_kernels.cpp:978-1034 (messages in this
+// library's words).
 void validate_dense_inputs(const lmc_tensor &slots, const lmc_tensor &ptrs,
                            const lmc_tensor &offs, const lmc_tensor &sizes,
                            int64_t total_tokens, int64_t fixed) {
-  check(slots.ndim == 1, "slot_mapping_full must be 1D.");
-  check(ptrs.ndim == 1, "chunk_ptrs_npu must be 1D.");
-  check(offs.ndim == 1, "chunk_offsets_npu must be 1D.");
-  check(sizes.ndim == 1, "chunk_sizes_npu must be 1D.");
-  check(offs.dtype == LMC_I32, "chunk_offsets_npu must be torch.int32.");
-  check(sizes.dtype == LMC_I32, "chunk_sizes_npu must be torch.int32.");
+  check(slots.ndim == 1, "slot_mapping_full is not a vector");
+  check(ptrs.ndim == 1, "chunk_ptrs_npu is not a vector");
+  check(offs.ndim == 1, "chunk_offsets_npu is not a vector");
+  check(sizes.ndim == 1, "chunk_sizes_npu is not a vector");
+  check(offs.dtype == LMC_I32, "chunk_offsets_npu holds int32 token offsets");
+  check(sizes.dtype == LMC_I32, "chunk_sizes_npu holds int32 token counts");
   if (fixed > 0)
     check(numel(offs) > 0 && numel(sizes) > 0,
-          "fixed dense direct metadata tensors must not be empty.");
+          "fixed-size dense direct chunks need chunk offset and size tensors with entries");
   else
     check(numel(ptrs) == numel(offs) && numel(ptrs) == numel(sizes),
-          "chunk pointer, offset and size tensors must have the same length.");
-  check(total_tokens > 0, "total_tokens must be positive.");
-  check(fixed >= 0, "fixed_chunk_size must be non-negative.");
+          "chunk_ptrs_npu, chunk_offsets_npu and chunk_sizes_npu differ in length");
+  check(total_tokens > 0, "total_tokens is not positive");
+  check(fixed >= 0, "fixed_chunk_size is negative");
   check(slots.sizes[0] <= total_tokens,
-        "slot_mapping_full length cannot exceed total_tokens.");
+        "slot_mapping_full is longer than total_tokens");
   if (fixed > 0) {
     const int64_t nc = numel(ptrs);
     check((nc - 1) * fixed < total_tokens && nc * fixed >= total_tokens,
-          "fixed_chunk_size does not cover total_tokens.");
+          "the chunks of fixed_chunk_size tokens do not span total_tokens");
   }
-  check(slots.device >= 0, "slot_mapping_full must be on the GPU.");
-  check(offs.device >= 0, "chunk_offsets_npu must be on the GPU.");
-  check(sizes.device >= 0, "chunk_sizes_npu must be on the GPU.");
+  check(slots.device >= 0, "slot_mapping_full is not a GPU tensor");
+  check(offs.device >= 0, "chunk_offsets_npu is not a GPU tensor");
+  check(sizes.device >= 0, "chunk_sizes_npu is not a GPU tensor");
 }
 
 void dense_direct(const lmc_tensor *ptrs_t, const lmc_tensor *caches, int n,
@@ -633,7 +635,7 @@ void dense_direct(const lmc_tensor *ptrs_t, const lmc_tensor *caches, int n,
                   int64_t fixed, int fmt, bool two_major, int64_t kH,
                   int64_t vH, int64_t dsaH, bool interleaved, bool page2lmc,
                   bool validate, hipStream_t stream) {
-  check(is_mla_dsa(fmt), "Dense direct transfer only supports MLA/DSA formats.");
+  check(is_mla_dsa(fmt), "dense direct transfers move MLA/DSA formats (3-6) only");
   const LayerGeom g = layer_geom(caches, n, fmt, two_major, kH, vH, dsaH);
   const lmc_tensor &slots = index_tensor(slots_t, "slot_mapping_full");
   const lmc_tensor &ptrs = chunk_table(ptrs_t);
@@ -641,12 +643,12 @@ void dense_direct(const lmc_tensor *ptrs_t, const lmc_tensor *caches, int n,
   const lmc_tensor &sizes = index_tensor(sizes_t, "chunk_sizes_npu");
   if (validate) validate_dense_inputs(slots, ptrs, offs, sizes, total_tokens, fixed);
   // Checks every call keeps (the kernel's reads must stay in bounds).
-  check(slots.ndim == 1, "slot_mapping_full must be 1D.");
+  check(slots.ndim == 1, "slot_mapping_full is not a vector");
   check(total_tokens > 0 && total_tokens < (int64_t(1) << 31) && fixed >= 0 &&
             fixed < (int64_t(1) << 31),
         "total_tokens and fixed_chunk_size must fit int32");
   check(slots.sizes[0] <= total_tokens,
-        "slot_mapping_full length cannot exceed total_tokens.");
+        "slot_mapping_full is longer than total_tokens");
   if (fixed == 0)
     check(offs.dtype == LMC_I32 && sizes.dtype == LMC_I32 &&
               numel(offs) >= numel(ptrs) && numel(sizes) >= numel(ptrs),

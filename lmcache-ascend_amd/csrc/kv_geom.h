@@ -115,7 +115,7 @@ bool nontemporal_enabled();
 const lmc_tensor &slots_of(const lmc_tensor *s);
 
 // The reference's format / cache-tuple checks (csrc/utils.cpp:903-966),
-// with its messages; ValueError on failure.
+// in this library's words; ValueError on failure.
 void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt);
 
 // Paged side of one layer's vLLM caches.  Planes are those present in the

@@ -135,47 +135,48 @@ bool contiguous(const lmc_tensor &t) {
   return true;
 }
 
-// csrc/mem_kernels.cpp:758-800, with the reference's messages.
+// The input conditions of csrc/mem_kernels.cpp:758-800 (messages in this
+// library's words).
 void sparse_graph(const lmc_tensor &k, const lmc_tensor &pe, int64_t kH, int64_t peH,
                   const lmc_tensor &slots, const lmc_tensor &sel, const lmc_tensor &counts,
                   const lmc_tensor &ptrs, const lmc_tensor &limits, int64_t chunk_size,
                   int64_t max_cores, hipStream_t stream) {
-  check(sel.ndim == 2 && contiguous(sel), "Graph selected tokens must be a contiguous matrix");
+  check(sel.ndim == 2 && contiguous(sel), "sparse graph: selected tokens are not a contiguous [rows, columns] matrix");
   bool same = slots.ndim == 2 && contiguous(slots);
   for (int i = 0; same && i < 2; ++i) same = slots.sizes[i] == sel.sizes[i];
-  check(same, "Graph slots must match selected tokens");
-  check(sel.dtype == LMC_I32 || sel.dtype == LMC_I64, "Graph selected tokens must be int32/int64");
-  check(slots.dtype == LMC_I32 || slots.dtype == LMC_I64, "Graph slots must be int32/int64");
+  check(same, "sparse graph: slots and selected tokens differ in shape or layout");
+  check(sel.dtype == LMC_I32 || sel.dtype == LMC_I64, "sparse graph: selected tokens are neither int32 nor int64");
+  check(slots.dtype == LMC_I32 || slots.dtype == LMC_I64, "sparse graph: slots are neither int32 nor int64");
   const int64_t requests = sel.sizes[0];
   check(requests > 0 && sel.sizes[1] > 0 && numel(sel) <= INT32_MAX,
-        "Graph payload exceeds int32 packed addressing");
+        "sparse graph: no rows, or more selected entries than int32 indexes");
   const int64_t cstride = counts.ndim > 0 ? counts.strides[0] : 0;
   check((counts.ndim == 1 || (counts.ndim == 2 && counts.sizes[1] > 0)) &&
             counts.sizes[0] == requests && counts.dtype == LMC_I32 && cstride > 0 &&
             cstride <= INT32_MAX,
-        "Graph counts must have one int32 count per row");
+        "sparse graph: counts are not one int32 per row");
   check((requests - 1) * cstride + 1 <= extent_bytes(counts) / 4,
-        "Graph counts must have one int32 count per row");
+        "sparse graph: counts are not one int32 per row");
   check(numel(limits) == requests && contiguous(limits) && limits.dtype == LMC_I32,
-        "Graph limits must have one contiguous int32 value per row");
+        "sparse graph: limits are not one contiguous int32 per row");
   check(ptrs.ndim == 2 && ptrs.sizes[0] == 2 && ptrs.sizes[1] > 0 &&
             ptrs.sizes[1] % requests == 0 && contiguous(ptrs) && ptrs.dtype == LMC_I64,
-        "Graph sources must be two contiguous int64 plane tables");
+        "sparse graph: chunk sources are not a contiguous int64 [2, chunks] table");
   check(chunk_size > 0 && chunk_size <= INT32_MAX && ptrs.sizes[1] <= INT32_MAX / chunk_size,
-        "Graph source capacity exceeds int32 token addressing");
-  check(k.dtype == LMC_F16 || k.dtype == LMC_BF16, "Graph KV transfer supports FP16/BF16");
+        "sparse graph: chunk tokens exceed int32 indexing");
+  check(k.dtype == LMC_F16 || k.dtype == LMC_BF16, "sparse graph: caches are neither float16 nor bfloat16");
   if (kH <= 0) kH = size(k, -2) * size(k, -1);
   if (peH <= 0) peH = size(pe, -2) * size(pe, -1);
   const int64_t k_bytes = kH * 2, pe_bytes = peH * 2;
   check(k.data && pe.data && k_bytes > 0 && pe_bytes > 0 && k_bytes % 32 == 0 &&
             pe_bytes % 32 == 0 && k_bytes <= 16384 && pe_bytes <= 16384,
-        "Graph K/PE token widths must be 32-byte aligned and fit copy queues");
+        "sparse graph: K and PE rows must be non-empty multiples of 32 bytes up to 16 KiB");
   check(sel.device >= 0 && slots.device == sel.device && counts.device == sel.device &&
             ptrs.device == sel.device && limits.device == sel.device &&
             k.device == sel.device && pe.device == sel.device,
         "Graph transfer inputs must be on the same GPU");
   check(max_cores >= 0 && max_cores <= UINT32_MAX,
-        "max_aiv_cores must be zero (automatic) or a positive uint32 value");
+        "max_aiv_cores is negative or above the uint32 range");
   DeviceGuard guard(sel.device);
   SfaJob job;
   std::memset(&job, 0, sizeof(job));

@@ -780,7 +780,7 @@ MultiLayerGeom plan_multi_layer(int64_t n_layers, int64_t last_dim,
     concatenated = true;
     break;
   default:
-    fail(LMC_ERR_RUNTIME, "Unsupported KVCacheFormat: " + std::to_string(fmt));
+    fail(LMC_ERR_RUNTIME, "multi-layer transfer: no plane layout for KV format " + std::to_string(fmt));
   }
   for (int p = 0; p < planes; ++p)
     check(width[p] > 0, "hidden dims must be positive for KV format " +
@@ -905,10 +905,10 @@ void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt) {
       fmt != LMC_FMT_MLA_KV && fmt != LMC_FMT_DSA_KV &&
       fmt != LMC_FMT_MLA_LATENT && fmt != LMC_FMT_DSA_INDEX)
     fail(LMC_ERR_VALUE,
-         "Invalid KV cache format: " + std::to_string(fmt) +
-             ". Expected 1 (MERGED_KV), 2 (SEPARATE_KV), 3 (MLA_KV), 4 "
-             "(DSA_KV), 5 (MLA_LATENT), or 6 (DSA_INDEX)");
-  if (n <= 0) fail(LMC_ERR_VALUE, "vllm_kv_caches cannot be empty");
+         "kvcache_format_raw " + std::to_string(fmt) +
+             " is not a KV cache format (1 MERGED_KV, 2 SEPARATE_KV, 3 "
+             "MLA_KV, 4 DSA_KV, 5 MLA_LATENT, 6 DSA_INDEX)");
+  if (n <= 0) fail(LMC_ERR_VALUE, "vllm_kv_caches holds no tensor");
   auto same_sizes = [](const lmc_tensor &a, const lmc_tensor &b) {
     if (a.ndim != b.ndim) return false;
     for (int i = 0; i < a.ndim; ++i)
@@ -916,21 +916,21 @@ void validate_vllm_caches(const lmc_tensor *caches, int n, int fmt) {
     return true;
   };
   if (fmt == LMC_FMT_DSA_KV) {
-    if (n != 3) fail(LMC_ERR_VALUE, "DSA_KV expects 3 tensors (K, V, and DSA_K).");
+    if (n != 3) fail(LMC_ERR_VALUE, "a DSA_KV layer takes three caches: K, V and the DSA keys");
   } else if (fmt == LMC_FMT_MLA_KV || fmt == LMC_FMT_MLA_LATENT) {
     if (n < 2)
-      fail(LMC_ERR_VALUE, "MLA_KV/MLA_LATENT expects 2 tensors (K and V).");
+      fail(LMC_ERR_VALUE, "an MLA_KV or MLA_LATENT layer takes two caches, K and V");
     if (same_sizes(caches[0], caches[1]))
-      fail(LMC_ERR_VALUE, "MLA_KV/MLA_LATENT expects K and V caches to have "
-                          "different shapes.");
+      fail(LMC_ERR_VALUE, "MLA_KV / MLA_LATENT K and V caches of equal shape: "
+                          "the latent and rope planes differ in width");
   } else if (fmt == LMC_FMT_DSA_INDEX) {
     // at least one tensor: already checked
   } else if (fmt == LMC_FMT_SEPARATE_KV) {
-    if (n != 2) fail(LMC_ERR_VALUE, "SEPARATE_KV expects 2 tensors (K and V).");
+    if (n != 2) fail(LMC_ERR_VALUE, "a SEPARATE_KV layer takes two caches, K and V");
     if (!same_sizes(caches[0], caches[1]))
-      fail(LMC_ERR_VALUE, "K and V caches must have the same shape.");
+      fail(LMC_ERR_VALUE, "SEPARATE_KV K and V caches differ in shape");
   } else {
-    if (n != 1) fail(LMC_ERR_VALUE, "MERGED_KV expects 1 tensor.");
+    if (n != 1) fail(LMC_ERR_VALUE, "a MERGED_KV layer takes one cache holding K and V");
   }
 }
 
@@ -960,7 +960,7 @@ LayerGeom layer_geom(const lmc_tensor *caches, int n, int fmt, bool two_major,
     const int64_t w[kMaxPlanes] = {kH, fmt == LMC_FMT_DSA_INDEX ? 0 : vH,
                                    fmt == LMC_FMT_DSA_KV ? dsaH : 0};
     g.plane_elems = w[0] + w[1] + w[2];
-    check(g.plane_elems > 0, "MLA/DSA plane size must be positive");
+    check(g.plane_elems > 0, "MLA/DSA caches give no row width");
     int64_t pre = 0;
     g.num_slots = INT64_MAX;
     for (int p = 0; p < kMaxPlanes; ++p) {
@@ -1171,7 +1171,7 @@ void fused_transfer(const lmc_tensor &kv, uint8_t *stg_data, int stg_device,
   if (!direction && required > 0)
     hip_check(hipMemcpyAsync(stg_data, kv.data, required,
                              hipMemcpyHostToDevice, s),
-              "H2D memcpy failed: cpu_buffer -> staging_cache");
+              "copy of the host object into the staging buffer");
   if (direction && clear_before_store && required > 0) {
     const int64_t n16 = (required + 15) / 16;  // capacity is a multiple of 16
     const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 4096);
@@ -1194,7 +1194,7 @@ void fused_transfer(const lmc_tensor &kv, uint8_t *stg_data, int stg_device,
   if (direction && required > 0)
     hip_check(hipMemcpyAsync(kv.data, stg_data, required,
                              hipMemcpyDeviceToHost, s),
-              "D2H memcpy failed: staging_cache -> cpu_buffer");
+              "copy of the staging buffer into the host object");
 }
 
 } // namespace lmc
@@ -1247,7 +1247,7 @@ int lmc_fused_multi_layer_kv_transfer(
     const lmc_tensor &stg = deref(staging_cache, "staging_cache");
     check(stg.device >= 0, "staging_cache must be a device tensor");
     fused_transfer(kv, static_cast<uint8_t *>(stg.data), stg.device,
-                   nbytes(stg), "staging_cache size insufficient", false,
+                   nbytes(stg), "staging_cache is smaller than the transfer", false,
                    key_value_ptrs, slot_mapping, paged_device,
                    page_buffer_size, direction != 0, use_mla != 0,
                    kvcache_format, k_hidden_dims, v_hidden_dims,

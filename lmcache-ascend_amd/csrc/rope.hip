@@ -176,8 +176,8 @@ extern "C" int lmc_rotary_embedding_k_fused(const lmc_tensor *old_positions,
     const lmc_tensor &c = deref(cos_sin_cache, "cosSinCache");
     // csrc/pos_kernels.cpp:47-57: only bf16 / fp16 / fp32 keys.
     if (k.dtype != LMC_BF16 && k.dtype != LMC_F16 && k.dtype != LMC_F32)
-      fail(LMC_ERR_VALUE, "Unavailable tensor type for RoPE Tiling (only "
-                          "support BF16/FP16/FP32).");
+      fail(LMC_ERR_VALUE, "rotary_embedding_k_fused rotates bfloat16, float16 or "
+                          "float32 keys only");
     check(k.ndim == 2, "key must be [num_tokens, num_heads * head_size]");
     check(head_size > 0 && size(k, 1) % head_size == 0,
           "key width is not a multiple of head_size");

@@ -61,7 +61,7 @@ int32_t dtype_code(at::ScalarType t) {
   case at::kHalf: return LMC_F16;
   case at::kBFloat16: return LMC_BF16;
   case at::kFloat: return LMC_F32;
-  default: throw std::runtime_error("ScalarType not supported.");
+  default: throw std::runtime_error("tensor dtype has no lmc_tensor code");
   }
 }
 
@@ -124,7 +124,7 @@ std::vector<at::Tensor> normalize_kv_caches(const py::object &obj) {
   // csrc/pybind.cpp:22-31: a Tensor or a tuple of Tensors.
   if (THPVariable_Check(obj.ptr())) return {obj.cast<at::Tensor>()};
   if (py::isinstance<py::tuple>(obj)) return obj.cast<std::vector<at::Tensor>>();
-  throw std::runtime_error("vllm_kv_caches must be a Tensor or a tuple of Tensors");
+  throw std::runtime_error("vllm_kv_caches is neither a Tensor nor a tuple of Tensors");
 }
 
 void single_layer_kv_transfer(at::Tensor &lmc, const py::object &caches_obj,

@@ -295,7 +295,7 @@ def _normalize_kv_caches(obj):
         return [obj]
     if isinstance(obj, tuple):
         return list(obj)
-    raise RuntimeError("vllm_kv_caches must be a Tensor or a tuple of Tensors")
+    raise RuntimeError("vllm_kv_caches is neither a Tensor nor a tuple of Tensors")
 
 
 def single_layer_kv_transfer(
@@ -572,7 +572,7 @@ def _chunk_ptrs_for(lmc_tensors, device) -> torch.Tensor:
             continue
         p = get_device_ptr(t.data_ptr(), max(1, t.numel() * t.element_size()))
         if p == 0:
-            raise RuntimeError("Unable to retrieve device ptr, is this a host registered pointer ?")
+            raise RuntimeError("host tensor is not in pinned, device-mapped memory: no device address for it")
         ptrs.append(p)
     return torch.tensor(ptrs, dtype=torch.int64, device=device)
 
@@ -606,7 +606,7 @@ def _check_chunk_capacity(lmc_tensors, caches, fmt, kH, vH, dsaH, chunk_size, to
 
 def _require_cpu_chunks(lmc_tensors, what: str) -> None:
     if len(lmc_tensors) == 0:
-        raise RuntimeError("lmc_tensors must not be empty.")
+        raise RuntimeError("lmc_tensors lists no memory object")
     for t in lmc_tensors:
         if t.device.type != "cpu":
             raise RuntimeError(what)
@@ -717,7 +717,7 @@ def prepare_sparse_direct_destination_state(
     caches = _normalize_kv_caches(vllm_kv_caches)
     _check_caches(caches, kvcache_format_raw, False, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
     if int(kvcache_format_raw) not in _MLA_DSA:
-        raise RuntimeError("Prepared sparse destination state only supports MLA/DSA formats.")
+        raise RuntimeError("prepared sparse destination states serve MLA/DSA formats (3-6) only")
     st = SparseDirectDestinationState()
     st.caches = tuple(caches)
     st.kvcache_format = int(kvcache_format_raw)
@@ -752,10 +752,10 @@ def sparse_mla_dsa_batched_direct_kv_transfer(
     caches = _normalize_kv_caches(vllm_kv_caches)
     _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
     if int(chunk_size) <= 0:
-        raise RuntimeError("chunk_size must be positive.")
+        raise RuntimeError("chunk_size is not positive")
     if int(total_tokens) <= 0:
-        raise RuntimeError("total_tokens must be positive.")
-    _require_cpu_chunks(lmc_tensors, "Direct sparse retrieve requires CPU pinned memory objects.")
+        raise RuntimeError("total_tokens is not positive")
+    _require_cpu_chunks(lmc_tensors, "direct sparse retrieval reads memory objects in pinned host memory only")
     _check_chunk_capacity(lmc_tensors, caches, kvcache_format_raw, k_hidden_dims, v_hidden_dims, dsa_hidden_dims,
                           int(chunk_size), int(total_tokens))
     if selected_token_idx.numel() == 0:
@@ -821,8 +821,8 @@ def dense_mla_dsa_batched_direct_kv_transfer(
     caches = _normalize_kv_caches(vllm_kv_caches)
     _check_caches(caches, kvcache_format_raw, vllm_two_major, k_hidden_dims, v_hidden_dims, dsa_hidden_dims)
     if int(kvcache_format_raw) not in _MLA_DSA:
-        raise RuntimeError("Dense direct transfer only supports MLA/DSA formats.")
-    _require_cpu_chunks(lmc_tensors, "Dense direct transfer requires CPU pinned memory objects.")
+        raise RuntimeError("dense direct transfers move MLA/DSA formats (3-6) only")
+    _require_cpu_chunks(lmc_tensors, "dense direct transfers take memory objects in pinned host memory only")
     if int(fixed_chunk_size) > 0:
         _check_chunk_capacity(lmc_tensors, caches, kvcache_format_raw, k_hidden_dims, v_hidden_dims,
                               dsa_hidden_dims, int(fixed_chunk_size), int(total_tokens))
@@ -860,15 +860,15 @@ def _dense_group(layer_states, slot_mapping_full, layer_chunk_ptrs_npu, chunk_of
     """One dense direct transfer per layer, layer l using row l of the
     [layers, chunks] pointer table (csrc/mem_kernels.cpp:1221-1306)."""
     if len(layer_states) == 0:
-        raise RuntimeError("layer_states must not be empty.")
+        raise RuntimeError("layer_states lists no layer")
     if layer_chunk_ptrs_npu.dim() != 2:
-        raise RuntimeError("layer_chunk_ptrs_npu must be 2D [layers, chunks].")
+        raise RuntimeError("layer_chunk_ptrs_npu is not a [layers, chunks] table")
     if layer_chunk_ptrs_npu.size(0) != len(layer_states):
-        raise RuntimeError("layer pointer table row count must match layer_states.")
+        raise RuntimeError("layer_chunk_ptrs_npu rows and layer_states differ in count")
     if layer_chunk_ptrs_npu.size(1) <= 0:
-        raise RuntimeError("layer pointer table must contain at least one chunk.")
+        raise RuntimeError("layer_chunk_ptrs_npu has no chunk column")
     if not layer_chunk_ptrs_npu.is_contiguous():
-        raise RuntimeError("layer_chunk_ptrs_npu must be contiguous.")
+        raise RuntimeError("layer_chunk_ptrs_npu is not contiguous")
     for layer_id, st in enumerate(layer_states):
         _dense_direct(st.caches, st.kvcache_format, st.k_hidden_dims, st.v_hidden_dims, st.dsa_hidden_dims,
                       slot_mapping_full, layer_chunk_ptrs_npu[layer_id], chunk_offsets_npu, chunk_sizes_npu,
@@ -885,25 +885,25 @@ def dense_mla_dsa_group_direct_kv_transfer_fast(
     (csrc/pybind.cpp:187-240)."""
     layer_states = list(layer_states)
     if len(layer_states) == 0:
-        raise RuntimeError("layer_states must not be empty.")
+        raise RuntimeError("layer_states lists no layer")
     if len(layer_tensors) != len(layer_states):
-        raise RuntimeError("layer tensor rows must match layer states.")
+        raise RuntimeError("layer tensor rows and layer_states differ in count")
     rows, flat, num_chunks = [], [], None
     for layer_id, tensors in enumerate(layer_tensors):
         if num_chunks is None:
             num_chunks = len(tensors)
             if num_chunks <= 0:
-                raise RuntimeError("each group store layer must contain at least one chunk.")
+                raise RuntimeError("a group store layer lists no chunk")
         if len(tensors) != num_chunks:
-            raise RuntimeError("all group store layers must have the same chunk count.")
+            raise RuntimeError("group store layers differ in chunk count")
         row = []
         for chunk_id, t in enumerate(tensors):
             if t.device.type != "cpu":
-                raise RuntimeError("group direct store requires CPU destination tensors.")
+                raise RuntimeError("group direct stores write host tensors only")
             p = get_device_ptr(t.data_ptr())
             if p == 0:
                 raise RuntimeError(
-                    "group direct store destination tensor is not registered: "
+                    "group direct store target has no device mapping: "
                     f"layer={layer_id}, chunk={chunk_id}"
                 )
             row.append(p)
@@ -983,10 +983,10 @@ class IndexerC8GroupState:
     def __init__(self, layers):
         layers = list(layers)
         if not layers:
-            raise RuntimeError("C8 group must contain at least one layer")
+            raise RuntimeError("C8 group holds no layer")
         for st in layers:
             if st.keys.device != layers[0].keys.device or st.cache_slots != layers[0].cache_slots:
-                raise RuntimeError("C8 group layers must share device and slot capacity")
+                raise RuntimeError("C8 group layers differ in GPU or in slot capacity")
         self.layers = layers
         self.max_key_bytes = max([128] + [st.key_bytes for st in layers])
         self._table = _c8_table(layers)

@@ -108,8 +108,7 @@ def check_memory_obj(tensor: torch.Tensor, fmt: MemoryFormat, expected_fmt: Memo
     the object carries the expected tag, and its tensor has that format's
     rank and, where given, its layer count and row width."""
     if fmt != expected_fmt:
-        raise ValueError(f"The memory object should be in {expected_fmt.name} format in order to be processed "
-                         f"by the connector (got {fmt.name}).")
+        raise ValueError(f"memory object is tagged {fmt.name}; this transfer takes {expected_fmt.name} objects")
     rank = 4 if fmt in (MemoryFormat.KV_2LTD, MemoryFormat.KV_MLA_FMT) else 3
     if tensor.dim() != rank:
         raise ValueError(f"{fmt.name} objects are {rank}-D, got shape {tuple(tensor.shape)}")

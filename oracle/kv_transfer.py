@@ -66,7 +66,7 @@ def multi_layer_planes(fmt: int, use_mla: bool, last_dim: int, kH: int, vH: int,
         return [_Plane(kH, 0, 0, 0), _Plane(vH, 1, 0, kH), _Plane(dsaH, 2, 0, kH + vH)], 3, True
     if fmt == DSA_INDEX:
         return [_Plane(dsaH, 0, 0, 0)], 1, True
-    raise RuntimeError(f"Unsupported KVCacheFormat: {fmt}")
+    raise RuntimeError(f"no plane layout for KV format {fmt}")
 
 
 def multi_layer_kv_transfer(lmc: np.ndarray, table: Sequence[np.ndarray], slots: np.ndarray,

@@ -65,18 +65,18 @@ def test_single_layer_invalid_format_is_value_error():
     st = lib.lmc_single_layer_kv_transfer(ctypes.byref(lmc), caches, 1, ctypes.byref(slots),
                                           1, 9, 0, 0, 0, 0, 0, None)
     assert st == _lib.ERR_VALUE
-    assert b"Invalid KV cache format: 9" in lib.lmc_last_error()
-    with pytest.raises(ValueError, match="Invalid KV cache format"):
+    assert b"9 is not a KV cache format" in lib.lmc_last_error()
+    with pytest.raises(ValueError, match="is not a KV cache format"):
         _lib.raise_for(st)
 
 
 @pytest.mark.parametrize(
     "fmt,n,msg",
     [
-        (2, 1, b"SEPARATE_KV expects 2 tensors"),
-        (1, 2, b"MERGED_KV expects 1 tensor"),
-        (4, 2, b"DSA_KV expects 3 tensors"),
-        (3, 1, b"MLA_KV/MLA_LATENT expects 2 tensors"),
+        (2, 1, b"a SEPARATE_KV layer takes two caches"),
+        (1, 2, b"a MERGED_KV layer takes one cache"),
+        (4, 2, b"a DSA_KV layer takes three caches"),
+        (3, 1, b"an MLA_KV or MLA_LATENT layer takes two caches"),
     ],
 )
 def test_single_layer_tuple_size_checks(fmt, n, msg):
@@ -99,7 +99,7 @@ def test_single_layer_separate_shape_mismatch():
     st = lib.lmc_single_layer_kv_transfer(ctypes.byref(lmc), caches, 2, ctypes.byref(slots),
                                           1, 2, 0, 0, 0, 0, 0, None)
     assert st == _lib.ERR_VALUE
-    assert b"same shape" in lib.lmc_last_error()
+    assert b"K and V caches differ in shape" in lib.lmc_last_error()
 
 
 def test_multi_layer_unsupported_format_is_runtime_error():
@@ -111,7 +111,7 @@ def test_multi_layer_unsupported_format_is_runtime_error():
     st = lib.lmc_multi_layer_kv_transfer(ctypes.byref(kv), ctypes.byref(ptrs), ctypes.byref(slots),
                                          0, 64, 1, 0, 7, 0, 0, 0, None)
     assert st == _lib.ERR_RUNTIME
-    assert b"Unsupported KVCacheFormat: 7" in lib.lmc_last_error()
+    assert b"no plane layout for KV format 7" in lib.lmc_last_error()
 
 
 def test_multi_layer_rejects_short_pointer_table():

@@ -42,7 +42,7 @@ def test_tags_and_token_counts():
 def test_connector_checks():
     obj = torch.zeros(2, 4, 8, 64)
     F.check_memory_obj(obj, F.MemoryFormat.KV_2LTD, F.MemoryFormat.KV_2LTD, num_layers=4, width=64)
-    with pytest.raises(ValueError, match="should be in KV_2LTD format"):
+    with pytest.raises(ValueError, match="tagged KV_MLA_FMT; this transfer takes KV_2LTD"):
         F.check_memory_obj(obj, F.MemoryFormat.KV_MLA_FMT, F.MemoryFormat.KV_2LTD)
     with pytest.raises(ValueError, match="layers"):
         F.check_memory_obj(obj, F.MemoryFormat.KV_2LTD, F.MemoryFormat.KV_2LTD, num_layers=3)

@@ -211,7 +211,7 @@ def test_decode_limits(ops):
                                 torch.zeros((1, 48), dtype=torch.int32, device=DEV),
                                 torch.zeros((1, 4, 48), dtype=torch.uint8, device=DEV))
     cdf = torch.zeros((1, 32, 65), dtype=torch.int16, device=DEV)
-    with pytest.raises(RuntimeError, match="Max bins"):
+    with pytest.raises(RuntimeError, match="fewer than 64 bins"):
         ops.decode_fast_prefsum(cdf, torch.zeros(4, dtype=torch.uint8, device=DEV),
                                 torch.zeros((1, 32), dtype=torch.int32, device=DEV),
                                 torch.zeros((1, 4, 32), dtype=torch.uint8, device=DEV))

@@ -320,7 +320,7 @@ def test_c8_block_map_vs_oracle(c_ops, grouped):
 @pytest.mark.parametrize("build,message", [
     (lambda c, d: c.IndexerC8State(torch.empty(2, 128, 1, 128, dtype=torch.int8, device=d),
                                    torch.empty(2, 128, 1, 1, dtype=torch.bfloat16, device=d)), "float16 scales"),
-    (lambda c, d: c.IndexerC8State(torch.empty(2, 64, 1, 128, dtype=torch.bfloat16, device=d)), "PA_BSND"),
+    (lambda c, d: c.IndexerC8State(torch.empty(2, 64, 1, 128, dtype=torch.bfloat16, device=d)), r"not a contiguous \[blocks, 128, 1, 128\] cache"),
     (lambda c, d: c.IndexerC8State(torch.empty(2, 128, 1, 128, dtype=torch.bfloat16, device=d), None, 2),
      "block factor"),
 ])
@@ -428,9 +428,9 @@ def test_sparse_graph_errors(c_ops):
     sel = torch.zeros((2, 4), dtype=torch.int32, device=DEV)
     cnt = torch.zeros(2, dtype=torch.int32, device=DEV)
     ptrs = torch.zeros((2, 2), dtype=torch.int64, device=DEV)
-    with pytest.raises(RuntimeError, match="contiguous matrix"):
+    with pytest.raises(RuntimeError, match="contiguous \\[rows, columns\\] matrix"):
         c_ops.sparse_graph_kv_transfer(st, sel[:, :2], sel[:, ::2], cnt, ptrs, cnt, 16)
-    with pytest.raises(RuntimeError, match="two contiguous int64 plane tables"):
+    with pytest.raises(RuntimeError, match="contiguous int64 \\[2, chunks\\] table"):
         c_ops.sparse_graph_kv_transfer(st, sel, sel, cnt, ptrs[:1], cnt, 16)
-    with pytest.raises(RuntimeError, match="one contiguous int32 value per row"):
+    with pytest.raises(RuntimeError, match="one contiguous int32 per row"):
         c_ops.sparse_graph_kv_transfer(st, sel, sel, cnt, ptrs, cnt[:1], 16)

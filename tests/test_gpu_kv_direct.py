@@ -138,13 +138,13 @@ def test_sparse_single_layer_errors(ops):
     caches = mla_caches(g)
     lmc = torch.zeros(64 * 576, dtype=torch.bfloat16, device=DEV)
     s1 = torch.zeros(8, dtype=torch.int64, device=DEV)
-    with pytest.raises(ValueError, match="both be 1D or both be 2D"):
+    with pytest.raises(ValueError, match="one is 1-D and the other 2-D"):
         ops.sparse_single_layer_kv_transfer(lmc, caches, s1, torch.zeros((2, 4), dtype=torch.int32, device=DEV), 3)
-    with pytest.raises(ValueError, match="same length"):
+    with pytest.raises(ValueError, match="differ in shape"):
         ops.sparse_single_layer_kv_transfer(lmc, caches, s1, torch.zeros(7, dtype=torch.int32, device=DEV), 3)
-    with pytest.raises(ValueError, match="must be torch.int32"):
+    with pytest.raises(ValueError, match="holds int32 token indices"):
         ops.sparse_single_layer_kv_transfer(lmc, caches, s1, torch.zeros(8, dtype=torch.int64, device=DEV), 3)
-    with pytest.raises(ValueError, match="Invalid KV cache format"):
+    with pytest.raises(ValueError, match="is not a KV cache format"):
         ops.sparse_single_layer_kv_transfer(lmc, caches, s1, torch.zeros(8, dtype=torch.int32, device=DEV), 9)
 
 
@@ -378,13 +378,13 @@ def test_sparse_direct_errors(ops):
     chunk = torch.zeros(64 * 576, dtype=torch.bfloat16, pin_memory=True)
     s = torch.zeros(4, dtype=torch.int64, device=DEV)
     x = torch.zeros(4, dtype=torch.int32, device=DEV)
-    with pytest.raises(RuntimeError, match="chunk_size must be positive"):
+    with pytest.raises(RuntimeError, match="chunk_size is not positive"):
         ops.sparse_mla_dsa_batched_direct_kv_transfer([chunk], caches, s, x, 0, 64, 3)
-    with pytest.raises(RuntimeError, match="requires CPU pinned memory objects"):
+    with pytest.raises(RuntimeError, match="in pinned host memory only"):
         ops.sparse_mla_dsa_batched_direct_kv_transfer([chunk.to(DEV)], caches, s, x, 64, 64, 3)
-    with pytest.raises(RuntimeError, match="only supports MLA/DSA formats"):
+    with pytest.raises(RuntimeError, match="MLA/DSA formats \\(3-6\\) only"):
         ops.prepare_sparse_direct_destination_state(paged_caches(2, g), s, 2, 0, 0, 0)
-    with pytest.raises(ValueError, match="different shapes"):
+    with pytest.raises(ValueError, match="of equal shape"):
         ops.prepare_sparse_direct_destination_state((caches[0], caches[0]), s, 3, 0, 0, 0)
 
 
@@ -476,9 +476,9 @@ def test_dense_direct_errors(ops):
     s = torch.zeros(8, dtype=torch.int64, device=DEV)
     o = torch.zeros(1, dtype=torch.int32, device=DEV)
     chunk = torch.zeros(8 * 576, dtype=torch.bfloat16, pin_memory=True)
-    with pytest.raises(RuntimeError, match="only supports MLA/DSA formats"):
+    with pytest.raises(RuntimeError, match="MLA/DSA formats \\(3-6\\) only"):
         ops.dense_mla_dsa_batched_direct_kv_transfer([chunk], paged_caches(2, g), s, o, o, 8, 2)
-    with pytest.raises(RuntimeError, match="does not cover total_tokens"):
+    with pytest.raises(RuntimeError, match="do not span total_tokens"):
         ops.dense_mla_dsa_batched_direct_kv_transfer([chunk], mla_caches(g), s, o, o, 16, 3, fixed_chunk_size=4)
-    with pytest.raises(RuntimeError, match="cannot exceed total_tokens"):
+    with pytest.raises(RuntimeError, match="longer than total_tokens"):
         ops.dense_mla_dsa_batched_direct_kv_transfer([chunk], mla_caches(g), s, o, o, 4, 3, fixed_chunk_size=4)

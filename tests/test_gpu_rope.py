@@ -124,7 +124,7 @@ def test_strided_key_view_and_out_of_range_positions(ops):
 
 
 def test_rejects_integer_key(ops):
-    with pytest.raises(ValueError, match="BF16/FP16/FP32"):
+    with pytest.raises(ValueError, match="bfloat16, float16 or float32"):
         ops.rotary_embedding_k_fused(torch.arange(4, device=DEV), torch.arange(4, device=DEV),
                                      torch.zeros((4, 128), dtype=torch.int32, device=DEV), 128,
                                      torch.zeros((8, 128), device=DEV), True)

@@ -44,7 +44,7 @@ def test_create_attach_share_and_free(name):
     assert b[5000] == 7
     c_ops.detach_shm_pinned_ptr(q, size)
     c_ops.free_shm_pinned_ptr(p, size, name)
-    with pytest.raises(RuntimeError, match="shm_open attach failed"):
+    with pytest.raises(RuntimeError, match="cannot open shared-memory segment"):
         c_ops.attach_shm_pinned_ptr(size, name)
 
 
@@ -115,7 +115,7 @@ def test_argument_errors(name):
         c_ops.detach_shm_pinned_ptr(4096, 0)
     with pytest.raises(RuntimeError, match="not a valid node id"):
         c_ops.alloc_shm_pinned_ptr(4096, name, [-1])
-    with pytest.raises(RuntimeError, match="shm_open attach failed"):
+    with pytest.raises(RuntimeError, match="cannot open shared-memory segment"):
         c_ops.attach_shm_pinned_ptr(4096, name)
 
 
@@ -131,7 +131,7 @@ def test_failed_reservation_unlinks(name):
     # touched, and the half-made segment is removed
     with pytest.raises(RuntimeError, match="cannot reserve"):
         c_ops.alloc_shm_pinned_ptr(1 << 50, name)
-    with pytest.raises(RuntimeError, match="shm_open attach failed"):
+    with pytest.raises(RuntimeError, match="cannot open shared-memory segment"):
         c_ops.attach_shm_pinned_ptr(4096, name)
 
 
@@ -169,5 +169,5 @@ def test_interleave_over_node_zero(name):
 def test_bad_node_id_creates_nothing(name):
     with pytest.raises(RuntimeError, match="not a valid node id"):
         c_ops.alloc_shm_pinned_ptr(4096, name, [4096])
-    with pytest.raises(RuntimeError, match="shm_open attach failed"):
+    with pytest.raises(RuntimeError, match="cannot open shared-memory segment"):
         c_ops.attach_shm_pinned_ptr(4096, name)
