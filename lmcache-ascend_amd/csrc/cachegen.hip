@@ -139,39 +139,40 @@ __device__ __forceinline__ void wave_sync_cdf() {
 }
 
 // LDS of cdf_tile_kernel: [staged symbols, later the compacted count lists]
-// [histogram [nb][64] u32] [count sums] [Kraft sums] [present symbols]
-// [rows [64][nb + 1] int16].
-__host__ __device__ constexpr int cdf_stage_words(int T, int nb) {
-  return ((T < kCdfPiece ? T : kCdfPiece) * 64 > nb * 256 ? ((T < kCdfPiece ? T : kCdfPiece) * 64 + 15) / 16 * 4
-                                                          : nb * 64);
-}
+// [histogram [nb][64] u32] [count sums] [Garsia-Wachs flags] [present
+// symbols] [partial interval sums [4][64]] [rows [64][nb + 1] int16].
+// The first area holds a staged piece (at most 256 x 64 bytes), the count
+// lists (nb <= 64 rows of 64 words) and the node-id mode's leaf sets (63
+// rows): 64 rows of 64 words whatever T and nb.
+__host__ __device__ constexpr int cdf_stage_words(int, int) { return 64 * 64; }
 __host__ __device__ constexpr int cdf_lds_bytes(int T, int nb) {
-  return 4 * (cdf_stage_words(T, nb) + nb * 64 + 3 * 64) + 64 * (nb + 1) * 2;
+  return 4 * (cdf_stage_words(T, nb) + nb * 64 + 3 * 64 + kCdfWaves * 64) + 64 * (nb + 1) * 2;
 }
 
 // Garsia-Wachs lengths for the streams of this lane's group (Q = 1: lane =
 // stream, one wave; Q = 4: four lanes per stream, 16 streams per wave).
-// Overwrites the stream's histogram entries with the tree's depths, and its
-// Kraft sum with 2^16 (a full code: nothing to repair), when the longest
-// depth fits the limit (8 bits for at most 256 counted symbols, else 12).
+// When the longest depth fits the limit (8 bits for at most 256 counted
+// symbols, else 12), overwrites the stream's histogram entries with
+// (depth << kLenShift) | count and sets its flag in `gwok`.
 template <int Q, int CAP, class It, int kBins>
-__device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint32_t *ksum, const uint32_t *nsum,
+__device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint32_t *gwok, const uint32_t *nsum,
                                            int nb, int stream, int g, int m_max) {
   uint32_t *col = hist + stream;
   uint32_t *lst = lists + stream;
-  // Compaction: the counts of the present symbols in symbol order.
+  // Compaction: the counts of the present symbols in symbol order.  Every
+  // symbol's count is written at the next free position (m <= s < nb), so
+  // an absent one is overwritten by the next present one or lies past the
+  // list; the lanes of a group write the same words.  No branches.
   uint64_t pres = 0;
   int m = 0;
-  {
-    uint32_t cs[kBins];
+  uint32_t cs[kBins];
 #pragma unroll
-    for (int s = 0; s < kBins; ++s) cs[s] = s < nb ? col[s * 64] & kCountMask : 0u;
+  for (int s = 0; s < kBins; ++s) cs[s] = s < nb ? col[s * 64] & kCountMask : 0u;
 #pragma unroll
-    for (int s = 0; s < kBins; ++s) {
-      if (s < nb && g == 0) lst[m * 64] = cs[s];
-      pres |= static_cast<uint64_t>(cs[s] != 0) << s;
-      m += cs[s] != 0 ? 1 : 0;
-    }
+  for (int s = 0; s < kBins; ++s) {
+    if (s < nb) lst[m * 64] = cs[s];
+    pres |= static_cast<uint64_t>(cs[s] != 0) << s;
+    m += cs[s] != 0 ? 1 : 0;
   }
   wave_sync_cdf();
   typename It::V a[CAP];
@@ -181,19 +182,32 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
     const uint32_t w = lst[(pos < nb ? pos : nb - 1) * 64];
     a[i] = pos < m ? It::leaf(w, pos) : It::inf();
   }
+  if constexpr (std::is_same<It, cggw::ItemId>::value) {
+    // Leaf sets by id over the dead list: leaf j's at word j.
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) lst[(Q * i + g) * 64] = 1u << (Q * i + g);
+  }
   cggw::Depths<typename It::L> dep;
-  cggw::run<Q, CAP, It>(a, g, m, m_max, dep);
+  cggw::run<Q, CAP, It>(a, g, m, m_max, dep, lst);
   const bool ok = m >= 2 && dep.over(nsum[stream] > 256u) == 0;
   if (!ok) return;
+  // Write-back by leaf: lane g takes leaves j = g, g + Q, ... in order; the
+  // symbol of leaf j is the j-th set bit of `pres`, found by clearing the
+  // lowest set bit Q times per leaf.  The depth is ORed into the entry (it
+  // holds the count alone); an absent symbol's entry stays 0.
+  uint64_t rem = pres;
 #pragma unroll
-  for (int s0 = 0; s0 < kBins; s0 += Q) {
-    const int s = s0 + g;
-    if (s < nb && ((pres >> s) & 1u)) {
-      const int j = __builtin_popcountll(pres & ((1ull << s) - 1ull));
-      col[s * 64] = (dep.depth(j) << kLenShift) | (col[s * 64] & kCountMask);
-    }
+  for (int k = 0; k + 1 < Q; ++k) rem = k < g ? rem & (rem - 1u) : rem;
+#pragma unroll
+  for (int i = 0; i < CAP; ++i) {
+    const int j = Q * i + g;
+    const bool leaf = rem != 0;
+    const int s = leaf ? __builtin_ctzll(rem) : 0;
+    atomicOr(&col[s * 64], leaf ? dep.depth(j) << kLenShift : 0u);
+#pragma unroll
+    for (int k = 0; k < Q; ++k) rem &= rem - 1u;
   }
-  if (g == 0) ksum[stream] = 1u << kPrec;
+  gwok[stream] = 1u;
 }
 
 // kBins: register capacity for per-symbol values (nb <= kBins); kExact: nb
@@ -213,9 +227,10 @@ __global__ void __launch_bounds__(kCdfThreads)
   uint8_t *tile = reinterpret_cast<uint8_t *>(lds);
   uint32_t *hist = lds + cdf_stage_words(T, nb);
   uint32_t *nsum = hist + nb * 64;   // per stream: symbol count
-  uint32_t *ksum = nsum + 64;        // per stream: Kraft sum (units of 2^-16)
-  uint32_t *msum = ksum + 64;        // per stream: present symbols
-  int16_t *rows = reinterpret_cast<int16_t *>(msum + 64);
+  uint32_t *gwok = nsum + 64;        // per stream: Garsia-Wachs lengths taken
+  uint32_t *msum = gwok + 64;        // per stream: present symbols
+  uint32_t *psum = msum + 64;        // [wave][stream]: partial interval sums
+  int16_t *rows = reinterpret_cast<int16_t *>(psum + kCdfWaves * 64);
   for (int i = tid; i < nb * 64 + 192; i += kCdfThreads) hist[i] = 0;
   for (int t0 = 0; t0 < T; t0 += kCdfPiece) {
     const int tc = T - t0 < kCdfPiece ? T - t0 : kCdfPiece;
@@ -266,44 +281,24 @@ __global__ void __launch_bounds__(kCdfThreads)
     }
   }
   __syncthreads();
-  // Derivation, spread over the waves: wave q takes symbols [j0, j1) of
-  // every stream (lane = stream).
+  // Count sums and present-symbol counts, spread over the waves: wave q
+  // takes symbols [j0, j1) of every stream (lane = stream).
   constexpr int kS = kBins / kCdfWaves;
   const int share = (nb + kCdfWaves - 1) / kCdfWaves;
   const int j0 = q * share;
   const int j1 = j0 + share < nb ? j0 + share : nb;
-  uint32_t cnt_j[kS];
   {
     uint32_t part = 0, present = 0;
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
-      cnt_j[k] = (k < share && j0 + k < j1) ? hist[(j0 + k) * 64 + lane] : 0u;
-      part += cnt_j[k];
-      present += cnt_j[k] != 0 ? 1u : 0u;
+      const uint32_t c = (k < share && j0 + k < j1) ? hist[(j0 + k) * 64 + lane] : 0u;
+      part += c;
+      present += c != 0 ? 1u : 0u;
     }
     if (lane < cnt && part) {
       atomicAdd(nsum + lane, part);
       atomicAdd(msum + lane, present);
     }
-  }
-  __syncthreads();
-  {
-    const uint32_t n = nsum[lane];
-    const int ln = 31 - __builtin_clz(n | 1u);
-    uint32_t kpart = 0;  // units of 2^-16
-#pragma unroll
-    for (int k = 0; k < kS; ++k) {
-      const uint32_t cs = cnt_j[k];
-      uint32_t x = 0;
-      if (cs) {
-        x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs)));
-        if ((static_cast<uint64_t>(cs) << x) < n) ++x;
-        x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
-        kpart += 1u << (kPrec - x);
-      }
-      if (k < share && j0 + k < j1) hist[(j0 + k) * 64 + lane] = (x << kLenShift) | cs;
-    }
-    if (lane < cnt && kpart) atomicAdd(ksum + lane, kpart);
   }
   __syncthreads();
   // Garsia-Wachs lengths; the mode depends on the block's largest number of
@@ -320,55 +315,98 @@ __global__ void __launch_bounds__(kCdfThreads)
     if (mm >= 2) {
       if (mm <= 16 && T < 65536) {
         if (q == static_cast<int>(blockIdx.x % kCdfWaves))
-          gw_lengths<1, 16, cggw::Item16, kBins>(hist, lists, ksum, nsum, nb, lane, 0, mm);
+          gw_lengths<1, 16, cggw::Item16, kBins>(hist, lists, gwok, nsum, nb, lane, 0, mm);
+      } else if (mm <= 32 && T < 65536) {
+        gw_lengths<4, 8, cggw::ItemId, kBins>(hist, lists, gwok, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
       } else if (mm <= 32) {
-        gw_lengths<4, 8, cggw::Item32, kBins>(hist, lists, ksum, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
+        gw_lengths<4, 8, cggw::Item32, kBins>(hist, lists, gwok, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
       } else if constexpr (kBins > 32) {
-        gw_lengths<4, 16, cggw::Item64, kBins>(hist, lists, ksum, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
+        gw_lengths<4, 16, cggw::Item64, kBins>(hist, lists, gwok, nsum, nb, q * 16 + lane / 4, lane & 3, mm);
       }
     }
   }
   __syncthreads();
-  if (q == static_cast<int>(blockIdx.x % kCdfWaves) && lane < cnt) {
-    const uint32_t *col = hist + lane;  // (length << kLenShift) | count
+  // Lengths and interval assignment, spread over the waves: wave q takes
+  // symbols [j0, j1) of every stream (lane = stream).  A Garsia-Wachs stream
+  // keeps its tree's depths; the others (one present symbol, no counted
+  // symbol, or a tree deeper than the limit) take the Shannon lengths
+  // ceil(log2(n / count)) clamped to [1, 12].  Each wave sums its symbols'
+  // widths 2^(16 - length) into LDS: for a Garsia-Wachs stream the lengths
+  // form a complete alphabetic code, so each symbol's interval starts at the
+  // sum of the widths before it, already aligned to its own width, and every
+  // wave writes its own symbols' entries; an absent symbol (length 0) takes
+  // the base of the next present one (or the end).
+  const bool gw = gwok[lane] != 0;
+  {
+    const uint32_t n = nsum[lane];
+    const int ln = 31 - __builtin_clz(n | 1u);
+    uint32_t len[kS];
+    uint32_t own = 0;
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      const bool in_range = k < share && j0 + k < j1;
+      const int s = in_range ? j0 + k : 0;
+      const uint32_t v = in_range ? hist[s * 64 + lane] : 0u;
+      const uint32_t cs = v & kCountMask;
+      uint32_t x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs | 1u)));
+      x += (static_cast<uint64_t>(cs) << x) < n ? 1u : 0u;
+      x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
+      x = gw ? v >> kLenShift : (cs ? x : 0u);
+      len[k] = x;
+      own += x ? 1u << (kPrec - x) : 0u;
+      if (in_range && !gw) hist[s * 64 + lane] = (x << kLenShift) | cs;
+    }
+    psum[q * 64 + lane] = own;
+    __syncthreads();
+    int16_t *row = rows + lane * (nb + 1);
+    if (gw) {
+      uint32_t pos = 0;
+#pragma unroll
+      for (int w = 0; w < kCdfWaves - 1; ++w) pos += w < q ? psum[w * 64 + lane] : 0u;
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        if (k < share && j0 + k < j1) {
+          row[j0 + k] = static_cast<int16_t>(static_cast<uint16_t>((pos | len[k]) & 0xFFFFu));
+          pos += len[k] ? 1u << (kPrec - len[k]) : 0u;
+        }
+      }
+    }
+    if (q == 0) row[nb] = 0;
+  }
+  // The Shannon streams, in one wave: the Kraft repair (lengthen the rarest
+  // present symbol below the cap, the last one among equals, until the code
+  // fits; only a length capped at 12 bits, more than 4096 counted symbols,
+  // can need it, so it runs out of line on the LDS column), then the aligned
+  // in-order assignment: a symbol's base is the running position `pos`, its
+  // width 2^(16 - length) capped by the lowest set bit of `pos` (the code
+  // lengthened to match).
+  if (q == static_cast<int>(blockIdx.x % kCdfWaves) && lane < cnt && !gw) {
+    uint32_t *wcol = hist + lane;  // (length << kLenShift) | count
+    uint32_t kraft = 0;            // units of 2^-16
+#pragma unroll
+    for (int w = 0; w < kCdfWaves; ++w) kraft += psum[w * 64 + lane];
+    while (kraft > (1u << kPrec)) {
+      int pick = -1;
+      uint32_t best = 0;
+#pragma unroll 1
+      for (int s = 0; s < nb; ++s) {
+        const uint32_t v = wcol[s * 64], ls = v >> kLenShift, cs = v & kCountMask;
+        if (ls != 0 && ls < kMaxLen && (pick < 0 || cs <= best)) {
+          pick = s;
+          best = cs;
+        }
+      }
+      if (pick < 0) break;
+      const uint32_t lp = wcol[pick * 64] >> kLenShift;
+      kraft -= 1u << (kPrec - lp - 1);
+      wcol[pick * 64] += 1u << kLenShift;
+    }
     uint32_t len[kBins];
 #pragma unroll
     for (int s = 0; s < kBins; ++s) {
-      const uint32_t v = col[(s < nb ? s : 0) * 64];  // every read issued before the first use
+      const uint32_t v = wcol[(s < nb ? s : 0) * 64];  // every read issued before the first use
       len[s] = s < nb ? v >> kLenShift : 0u;
     }
-    // Kraft repair of the Shannon fallback: lengthen the rarest present
-    // symbol below the cap (the last one among equals) until the code fits.
-    // Needs a length capped at 12 bits (more than 4096 counted symbols), so
-    // it runs out of line on the LDS copy of (length, count) and is kept out
-    // of the unrolled code.
-    uint32_t kraft = ksum[lane];
-    if (kraft > (1u << kPrec)) {
-      uint32_t *wcol = hist + lane;
-      while (kraft > (1u << kPrec)) {
-        int pick = -1;
-        uint32_t best = 0;
-#pragma unroll 1
-        for (int s = 0; s < nb; ++s) {
-          const uint32_t v = wcol[s * 64], ls = v >> kLenShift, cs = v & kCountMask;
-          if (ls != 0 && ls < kMaxLen && (pick < 0 || cs <= best)) {
-            pick = s;
-            best = cs;
-          }
-        }
-        if (pick < 0) break;
-        const uint32_t lp = wcol[pick * 64] >> kLenShift;
-        kraft -= 1u << (kPrec - lp - 1);
-        wcol[pick * 64] += 1u << kLenShift;
-      }
-#pragma unroll
-      for (int s = 0; s < kBins; ++s) len[s] = s < nb ? col[s * 64] >> kLenShift : 0u;
-    }
-    // Aligned in-order assignment.  A symbol's base is the running position
-    // `pos`, its width 2^(16 - length) capped by the lowest set bit of `pos`
-    // (the code lengthened to match; never for the Garsia-Wachs lengths);
-    // an absent symbol (length 0) gets the same value, which is the base of
-    // the next present symbol (or the end).
     int16_t *row = rows + lane * (nb + 1);
     uint32_t pos = 0;
 #pragma unroll
@@ -383,7 +421,6 @@ __global__ void __launch_bounds__(kCdfThreads)
         pos += shrink ? low : w0;
       }
     }
-    row[nb] = 0;
   }
   __syncthreads();
   // The block's rows are contiguous in the output.

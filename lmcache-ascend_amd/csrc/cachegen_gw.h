@@ -22,6 +22,8 @@
 
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace lmc {
 namespace cggw {
 
@@ -224,30 +226,131 @@ __device__ __forceinline__ void step(typename It::V (&a)[CAP], int g, bool activ
   dep.add(active ? It::leaves(sum) : typename It::L(0));
 }
 
+// Up to 32 leaves in a quad, weights below 2^16, by node id:
+// (weight << 16) | id, leaves 0..31 and the node made by step t 32 + t.
+// Items no longer carry their leaf sets: the stream's LDS column (stride
+// 64 words) holds the set of every id, leaf j's {j} at word j and node
+// 32 + t's at word 32 + t, stored by step t, so that the list moves 32-bit
+// values.
+struct ItemId {
+  using V = uint32_t;
+  using L = uint32_t;
+  static constexpr uint32_t kInf = 0xFFFFu;
+  static __device__ __forceinline__ V leaf(uint32_t w, int j) { return (w << 16) | static_cast<uint32_t>(j); }
+  static __device__ __forceinline__ V inf() { return 0xFFFFFFFFu; }
+  static __device__ __forceinline__ uint32_t weight(V v) { return v >> 16; }
+};
+
+// One combination step by node id for a quad (Q = 4) over at most 4 * S
+// items; `t`: the step's index (wave-uniform), `tmax`: the last step's,
+// `sets`: the stream's LDS column of leaf sets by id (33 + tmax words).  The
+// list update is that of step(); the pair's leaf sets are read while the
+// new list is formed, and the new node's set is stored and counted at the
+// end.
+template <int S, int CAP>
+__device__ __forceinline__ void step_ids(uint32_t (&a)[CAP], int g, bool active, int t, int tmax, uint32_t *sets,
+                                         Depths<uint32_t> &dep) {
+  constexpr int Q = 4;
+  using It = ItemId;
+  static_assert(S <= CAP, "slots");
+  uint32_t up1[S], dn1[S], up2[S];
+  {
+    uint32_t r1[S], r2[S], r3[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      r1[i] = qp<kRot1>(a[i]);
+      r3[i] = qp<kRot3>(a[i]);
+      r2[i] = qp<kRot2>(a[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const uint32_t next1 = i + 1 < S ? r1[i + 1 < S ? i + 1 : 0] : It::inf();
+      const uint32_t prev3 = i > 0 ? r3[i > 0 ? i - 1 : 0] : It::inf();
+      const uint32_t next2 = i + 1 < S ? r2[i + 1 < S ? i + 1 : 0] : It::inf();
+      up1[i] = g == 3 ? next1 : r1[i];
+      dn1[i] = g == 0 ? prev3 : r3[i];
+      up2[i] = g >= 2 ? next2 : r2[i];
+    }
+  }
+  // The first position k whose triple qualifies, and the pair there.
+  int kslot = -1;
+  uint32_t xs = 0, ys = 0;
+#pragma unroll
+  for (int i = S - 1; i >= 0; --i) {
+    const bool c = It::weight(a[i]) <= It::weight(up2[i]);
+    kslot = c ? i : kslot;
+    xs = c ? a[i] : xs;
+    ys = c ? up1[i] : ys;
+  }
+  const uint32_t kq = kslot >= 0 ? static_cast<uint32_t>(Q * kslot + g) : 0x3FFu;
+  const int k = static_cast<int>(quad_min(kq));
+  const bool own = kq == static_cast<uint32_t>(k);
+  const uint32_t x = quad_or<Item16>(own ? xs : 0u);
+  const uint32_t y = quad_or<Item16>(own ? ys : 0u);
+  // The pair's leaf sets, by id (ids clamped for the padding items of a
+  // finished stream).
+  const uint32_t top = static_cast<uint32_t>(32 + tmax);
+  const uint32_t ix = min(x & 0xFFFFu, top), iy = min(y & 0xFFFFu, top);
+  const uint32_t sx = sets[ix * 64];
+  const uint32_t sy = sets[iy * 64];
+  const uint32_t sw = It::weight(x) + It::weight(y);
+  const uint32_t sum = (sw << 16) | static_cast<uint32_t>(32 + t);
+  // Re-insertion point: right after the last position before k whose
+  // weight is >= the combined weight (0 when none is).
+  const int kg = k - g;
+  int pslot = -1;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const bool c = Q * i < kg && It::weight(a[i]) >= sw;
+    pslot = c ? i : pslot;
+  }
+  const uint32_t pq = pslot >= 0 ? static_cast<uint32_t>(Q * pslot + g + 1) : 0u;
+  const int p = static_cast<int>(quad_max(pq));
+  const int pg = p - g;
+  uint32_t na[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    uint32_t v = Q * i <= kg ? dn1[i] : up1[i];
+    v = Q * i == pg ? sum : v;
+    na[i] = Q * i < pg ? a[i] : v;
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) a[i] = na[i];
+  const uint32_t set = sx | sy;
+  sets[(32 + t) * 64] = set;
+  dep.add(active ? set : 0u);
+}
+
 // Combination steps while the wave's longest list has more than Q * (S - 1)
 // items, then the phase with one slot fewer.  M: the wave's longest list
 // (wave-uniform); t: steps taken; m_lane: this stream's present symbols.
 template <int Q, int S, int CAP, class It>
-__device__ __forceinline__ void phases(typename It::V (&a)[CAP], int g, int m_lane, int &M, int &t,
-                                       Depths<typename It::L> &dep) {
+__device__ __forceinline__ void phases(typename It::V (&a)[CAP], int g, int m_lane, int &M, int &t, int tmax,
+                                       Depths<typename It::L> &dep, uint32_t *sets) {
   if constexpr (S >= 1) {
     while (M >= 2 && M > Q * (S - 1)) {
-      step<Q, S, CAP, It>(a, g, t < m_lane - 1, dep);
+      if constexpr (std::is_same<It, ItemId>::value)
+        step_ids<S, CAP>(a, g, t < m_lane - 1, t, tmax, sets, dep);
+      else
+        step<Q, S, CAP, It>(a, g, t < m_lane - 1, dep);
       --M;
       ++t;
     }
-    phases<Q, S - 1, CAP, It>(a, g, m_lane, M, t, dep);
+    phases<Q, S - 1, CAP, It>(a, g, m_lane, M, t, tmax, dep, sets);
   }
 }
 
 // Leaf depths of one stream's Garsia-Wachs tree, its first m_lane items in
 // a[] (the rest padding); m_max: the longest list of the wave, uniform.
+// `sets`: for ItemId, the stream's LDS column of leaf sets by id (the
+// leaves' written by the caller; 31 + m_max words at stride 64), otherwise
+// unused.
 template <int Q, int CAP, class It>
 __device__ __forceinline__ void run(typename It::V (&a)[CAP], int g, int m_lane, int m_max,
-                                    Depths<typename It::L> &dep) {
+                                    Depths<typename It::L> &dep, uint32_t *sets = nullptr) {
   int M = __builtin_amdgcn_readfirstlane(m_max);
   int t = 0;
-  phases<Q, CAP, CAP, It>(a, g, m_lane, M, t, dep);
+  phases<Q, CAP, CAP, It>(a, g, m_lane, M, t, M - 2, dep, sets);
 }
 
 }  // namespace cggw
