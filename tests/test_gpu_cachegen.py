@@ -455,3 +455,28 @@ def test_calculate_cdf_modes_vs_oracle(ops, case):
     want = oc.calculate_cdf(syms, nb)
     torch.cuda.synchronize()
     assert np.array_equal(cdf.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("nb", [1, 2, 3, 5, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64])
+def test_calculate_cdf_bin_count_sweep_vs_oracle(ops, nb):
+    """Every bin count from 1 to 64 that changes a bound in the kernel (the
+    per-wave symbol shares, the register capacity of 32 or 64 bins, exact
+    or not, the one-lane / node-id / 64-leaf step modes), with skewed
+    histograms (Dirichlet weights, so some symbols are absent and some
+    trees exceed the 8-bit limit), token counts around the 256-token piece,
+    out-of-range symbols and a partial block of channels: bit-exact against
+    the oracle."""
+    rng = np.random.default_rng(700 + nb)
+    for T in (1, 7, 256, 300):
+        L, C = 2, 80
+        syms = np.empty((L, T, C), np.uint8)
+        for l in range(L):
+            for c in range(C):
+                p = rng.dirichlet(np.full(nb, float(rng.choice([0.1, 0.5, 3.0]))))
+                syms[l, :, c] = rng.choice(nb, size=T, p=p)
+        syms[1, :, 3] = nb + 2                # not counted
+        d = torch.from_numpy(syms).to(DEV)
+        cdf = ops.calculate_cdf(d, nb)
+        want = oc.calculate_cdf(syms, nb)
+        torch.cuda.synchronize()
+        assert np.array_equal(cdf.cpu().numpy(), want), (nb, T)
