@@ -262,6 +262,24 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
     if (i >= sg.count) continue;
     const int64_t j = sg.tok0 + i;
     const int64_t slot = idx_at(job.slots, job.slot_i32, j);
+    // Reads that do not depend on the slot are issued before it is checked:
+    // a K row's positions and, for device objects, the row's first kU
+    // pieces, so the slot, position and row reads are in flight together
+    // (with a 2 KiB row the row loop below then loads nothing).  Measured
+    // on MI355X, 32 Llama-3-8B-shape layers with device objects and
+    // re-rotation, one call per layer (event time): 0.392 -> 0.363 ms.
+    int64_t po = -1, pn = -1;
+    if (ROPE && p0 == 0) {
+      po = idx_at(job.old_pos, job.pos_i32, j);
+      pn = idx_at(job.new_pos, job.pos_i32, j);
+    }
+    V pre[kU];
+    const uint8_t *src0 = reinterpret_cast<const uint8_t *>(sg.src) + p0 * sg.plane_bytes + i * rb;
+    if (kU > 1 && sg.src != 0) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (q * 16 + u * 256 < rb) pre[u] = gload(reinterpret_cast<const V *>(src0 + q * 16 + u * 256));
+    }
     if (slot < 0 || slot >= job.num_slots) continue;
     int64_t blk = 0, in_blk = slot;
     if (job.block_size > 0) {
@@ -273,8 +291,6 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
     bool rotate = false;
     Pack<CS, kPairs> co{}, so{}, cn{}, sn{};
     if (ROPE && p0 == 0) {
-      const int64_t po = idx_at(job.old_pos, job.pos_i32, j);
-      const int64_t pn = idx_at(job.new_pos, job.pos_i32, j);
       rotate = sg.src != 0 && po >= 0 && po < job.max_pos && pn >= 0 && pn < job.max_pos;
       if (rotate) {
         const CS *crow_o = static_cast<const CS *>(job.cache) + po * job.rot;
@@ -309,9 +325,14 @@ __global__ void __launch_bounds__(kBlendThreads) blend_layer_groups(const BlendJ
 #pragma unroll 1
       for (int64_t base = static_cast<int64_t>(q) * 16; base < rb; base += kU * 256) {
         V raw[kU];
+        if (kU > 1 && base == static_cast<int64_t>(q) * 16) {
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
-          if (base + u * 256 < rb) raw[u] = gload(reinterpret_cast<const V *>(src + base + u * 256));
+          for (int u = 0; u < kU; ++u) raw[u] = pre[u];  // read before the slot check
+        } else {
+#pragma unroll
+          for (int u = 0; u < kU; ++u)
+            if (base + u * 256 < rb) raw[u] = gload(reinterpret_cast<const V *>(src + base + u * 256));
+        }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
           const int64_t o = base + u * 256;
