@@ -320,8 +320,13 @@ int lmc_check_kv_caches(const lmc_tensor *caches, int32_t n_caches,
 
 /* Replaces calculate_cdf (csrc/cachegen_kernels.cpp:119-155; pybind
  * csrc/pybind.cpp:480).  input: [L, T, C] u8/i8 symbols.  output: a
- * caller-allocated int16 [L, C, n_bins + 1] tensor (the reference allocates
- * it with torch::zeros; the Python layer does the same before this call). */
+ * caller-allocated int16 [L, C, n_bins + 1] tensor, every entry of which is
+ * written (the reference allocates it with torch::zeros; the Python layer
+ * allocates it without a fill).  Each row is a CDF of aligned power-of-two
+ * intervals in symbol order with the code length in the low 4 bits: the
+ * lengths of an optimal alphabetic code (Garsia-Wachs) when the longest
+ * fits 8 bits (at most 256 counted symbols) or 12 (more), else Shannon
+ * lengths clamped to [1, 12]. */
 int lmc_calculate_cdf(const lmc_tensor *input, int32_t n_bins,
                       const lmc_tensor *output, void *stream);
 
