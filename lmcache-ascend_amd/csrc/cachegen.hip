@@ -152,8 +152,8 @@ __host__ __device__ constexpr int cdf_lds_bytes(int T, int nb) {
 // Garsia-Wachs lengths for the streams of this lane's group (Q = 1: lane =
 // stream, one wave; Q = 4: four lanes per stream, 16 streams per wave).
 // When the longest depth fits the limit (8 bits for at most 256 counted
-// symbols, else 12), overwrites the stream's histogram entries with
-// (depth << kLenShift) | count and sets its flag in `gwok`.
+// symbols, else 12), stores the leaf depths' bit-sliced counters and the
+// presence mask in the stream's list column and sets its flag in `gwok`.
 template <int Q, int CAP, class It, int kBins>
 __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint32_t *gwok, const uint32_t *nsum,
                                            int nb, int stream, int g, int m_max) {
@@ -191,22 +191,18 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
   cggw::run<Q, CAP, It>(a, g, m, m_max, dep, lst);
   const bool ok = m >= 2 && dep.over(nsum[stream] > 256u) == 0;
   if (!ok) return;
-  // Write-back by leaf: lane g takes leaves j = g, g + Q, ... in order; the
-  // symbol of leaf j is the j-th set bit of `pres`, found by clearing the
-  // lowest set bit Q times per leaf.  The depth is ORed into the entry (it
-  // holds the count alone); an absent symbol's entry stays 0.
-  uint64_t rem = pres;
+  // The lengths phase reads the depths by leaf from the stream's (dead)
+  // list column: rows 0-3 the counters' low words, 4-7 their high words,
+  // 8-9 the presence mask (the lanes of a group hold the same values).
+  using L = typename It::L;
+  const L d[4] = {dep.d0, dep.d1, dep.d2, dep.d3};
 #pragma unroll
-  for (int k = 0; k + 1 < Q; ++k) rem = k < g ? rem & (rem - 1u) : rem;
-#pragma unroll
-  for (int i = 0; i < CAP; ++i) {
-    const int j = Q * i + g;
-    const bool leaf = rem != 0;
-    const int s = leaf ? __builtin_ctzll(rem) : 0;
-    atomicOr(&col[s * 64], leaf ? dep.depth(j) << kLenShift : 0u);
-#pragma unroll
-    for (int k = 0; k < Q; ++k) rem &= rem - 1u;
+  for (int k = 0; k < 4; ++k) {
+    lst[k * 64] = static_cast<uint32_t>(d[k]);
+    lst[(4 + k) * 64] = static_cast<uint32_t>(static_cast<uint64_t>(d[k]) >> 32);
   }
+  lst[8 * 64] = static_cast<uint32_t>(pres);
+  lst[9 * 64] = static_cast<uint32_t>(pres >> 32);
   gwok[stream] = 1u;
 }
 
@@ -340,6 +336,14 @@ __global__ void __launch_bounds__(kCdfThreads)
   {
     const uint32_t n = nsum[lane];
     const int ln = 31 - __builtin_clz(n | 1u);
+    // A Garsia-Wachs stream's depths by leaf (the leaf of symbol s is the
+    // number of present symbols below it).
+    const uint32_t *dcol = lds + lane;
+    uint64_t dsl[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      dsl[k] = static_cast<uint64_t>(dcol[k * 64]) | (static_cast<uint64_t>(dcol[(4 + k) * 64]) << 32);
+    const uint64_t pres = static_cast<uint64_t>(dcol[8 * 64]) | (static_cast<uint64_t>(dcol[9 * 64]) << 32);
     uint32_t len[kS];
     uint32_t own = 0;
 #pragma unroll
@@ -351,7 +355,20 @@ __global__ void __launch_bounds__(kCdfThreads)
       uint32_t x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs | 1u)));
       x += (static_cast<uint64_t>(cs) << x) < n ? 1u : 0u;
       x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
-      x = gw ? v >> kLenShift : (cs ? x : 0u);
+      const int j = kBins <= 32 ? __builtin_popcount(static_cast<uint32_t>(pres) & ((1u << s) - 1u))
+                                : __builtin_popcountll(pres & ((1ull << s) - 1ull));
+      uint32_t depth;
+      if constexpr (kBins <= 32) {
+        const int jj = j & 31;
+        depth = ((static_cast<uint32_t>(dsl[0]) >> jj) & 1u) | (((static_cast<uint32_t>(dsl[1]) >> jj) & 1u) << 1) |
+                (((static_cast<uint32_t>(dsl[2]) >> jj) & 1u) << 2) |
+                (((static_cast<uint32_t>(dsl[3]) >> jj) & 1u) << 3);
+      } else {
+        const int jj = j & 63;
+        depth = static_cast<uint32_t>(((dsl[0] >> jj) & 1u) | (((dsl[1] >> jj) & 1u) << 1) |
+                                      (((dsl[2] >> jj) & 1u) << 2) | (((dsl[3] >> jj) & 1u) << 3));
+      }
+      x = cs ? (gw ? depth : x) : 0u;
       len[k] = x;
       own += x ? 1u << (kPrec - x) : 0u;
       if (in_range && !gw) hist[s * 64 + lane] = (x << kLenShift) | cs;
