@@ -300,13 +300,18 @@ __global__ void __launch_bounds__(kCdfThreads)
   // Garsia-Wachs lengths; the mode depends on the block's largest number of
   // present symbols, the same in every wave.
   {
+    // The wave's maximum by DPP within each 16-lane row (quad, half-row
+    // mirror, row mirror), then the four rows' lane 0 by readlane.
     uint32_t m_max = msum[lane];
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m_max), d, 64));
-      m_max = o > m_max ? o : m_max;
-    }
-    const int mm = __builtin_amdgcn_readfirstlane(static_cast<int>(m_max));
+    m_max = max(m_max, cggw::qp<cggw::kSwap>(m_max));
+    m_max = max(m_max, cggw::qp<cggw::kRot2>(m_max));
+    m_max = max(m_max, cggw::qp<0x141>(m_max));  // row_half_mirror
+    m_max = max(m_max, cggw::qp<0x140>(m_max));  // row_mirror
+    const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 0));
+    const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 16));
+    const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 32));
+    const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 48));
+    const int mm = static_cast<int>(max(max(r0, r1), max(r2, r3)));
     uint32_t *lists = lds;  // the staged symbols are dead
     if (mm >= 2) {
       if (mm <= 16 && T < 65536) {
