@@ -110,18 +110,21 @@ __device__ __forceinline__ void unpack_row(const int16_t *row, int nb,
 // calculate_cdf: 64 streams per block, four waves.  The block's symbols are
 // staged into LDS 256 tokens at a time ([tokens][64] u8, 16-byte loads); wave
 // q counts the q-th quarter of each staged piece into per-stream LDS
-// histogram columns (no-return adds, one column per lane).  The derivation
-// is then spread over the waves: wave q takes symbols [j0, j1) of every
-// stream (lane = stream) for the count sums, the present-symbol counts, the
-// Shannon lengths of the fallback (the smallest l with count << l >= n, from
-// two leading-zero counts) and their Kraft sums.  The Garsia-Wachs lengths
-// (cachegen_gw.h) replace the Shannon ones of every stream whose tree fits
-// the length limit: one lane per stream in one wave when no stream of the
-// block has more than 16 present symbols, a quad of lanes per stream in all
-// four waves otherwise.  One wave, rotating with the block index so that the
-// blocks of a CU use different SIMDs, then makes the serial aligned
-// assignment (the width of each interval capped by the lowest set bit of the
-// running base), and the block's 64 rows, contiguous in the output, leave as
+// histogram columns (no-return adds, one column per lane).  Wave q then
+// takes symbols [j0, j1) of every stream (lane = stream) for the count sums
+// and present-symbol counts.  The Garsia-Wachs steps (cachegen_gw.h) run
+// next: one lane per stream in one wave (rotating with the block index, so
+// that the blocks of a CU use different SIMDs) when no stream of the block
+// has more than 16 present symbols, a quad of lanes per stream in all four
+// waves otherwise; a stream whose tree fits the length limit leaves its
+// depth counters in LDS and a flag.  The waves again take a quarter of the
+// symbols each for the lengths (the tree's depths, or the Shannon lengths,
+// the smallest l with count << l >= n from two leading-zero counts) and the
+// partial sums of the interval widths, from which every wave writes the
+// intervals of its symbols of the Garsia-Wachs streams; the rotating wave
+// makes the serial aligned assignment of the other streams (the width of
+// each interval capped by the lowest set bit of the running base, after the
+// Kraft repair).  The block's 64 rows, contiguous in the output, leave as
 // coalesced dword stores.
 constexpr int kCdfWaves = 4;
 constexpr int kCdfThreads = 64 * kCdfWaves;
