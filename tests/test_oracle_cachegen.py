@@ -222,13 +222,14 @@ def _intervals(cdf_row_u16):
     return base, lens
 
 
-def _check_structure(row, counts):
+def _check_structure(row, counts, full=False):
     """Structural invariants of one CDF row: present symbols (and only they)
     have lengths 1..12 (at most 8 when at most 256 symbols are counted);
     each interval is aligned to its width (a fixed code); the intervals are
     gap-free in symbol order (the first starts at 0, each starts where the
     previous present symbol's ends), so the last one ends at the sum of the
-    widths, which is at most 0x10000 (Kraft <= 1)."""
+    widths, which is at most 0x10000 (Kraft <= 1), and exactly 0x10000 for
+    a code that is a full binary tree (`full`: the Garsia-Wachs rows)."""
     n = int(sum(counts))
     base, lens = _intervals(row)
     assert all((ln > 0) == bool(c) for ln, c in zip(lens, counts)), "present <=> length"
@@ -243,6 +244,8 @@ def _check_structure(row, counts):
             end = base[s] + w
             total += w
     assert end == total <= 0x10000, "Kraft"
+    if full:
+        assert total == 0x10000, "complete code"
 
 
 # Counts that force the Shannon fallback: a Fibonacci run makes a caterpillar
@@ -274,9 +277,14 @@ def test_cdf_structural_invariants(seed):
     p = rng.dirichlet(np.full(nb, 0.2))
     syms = rng.choice(nb, size=(3, 256, 64), p=p).astype(np.uint8)
     cdf = oc.calculate_cdf(syms, nb).view(np.uint16)
+    full_rows = 0
     for l in range(3):
         for c in range(64):
-            _check_structure(cdf[l, c], np.bincount(syms[l, :, c], minlength=nb))
+            counts = np.bincount(syms[l, :, c], minlength=nb)
+            full = int((counts > 0).sum()) >= 2 and _py_lengths(counts.tolist())[1]
+            full_rows += full
+            _check_structure(cdf[l, c], counts, full)
+    assert full_rows > 0
     for counts in _fallback_cases(rng, 8):
         assert not _py_lengths(counts)[1]
         _check_structure(_cdf_of_counts(counts), counts)
