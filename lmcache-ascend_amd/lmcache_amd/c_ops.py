@@ -373,8 +373,12 @@ def reshape_and_cache_back_flash(key_value, key_cache, value_cache, slot_mapping
 
 def calculate_cdf(input: torch.Tensor, n_bins: int) -> torch.Tensor:
     """csrc/cachegen_kernels.cpp:119-155: int16 [L, C, n_bins + 1] CDF of the
-    [L, T, C] symbols.  The reference zero-fills the output first; the
-    kernels write every entry of it, so it is allocated without a fill."""
+    [L, T, C] symbols, one row per (layer, channel) stream: aligned
+    power-of-two intervals in symbol order, the code length in the low 4
+    bits, the lengths those of an optimal alphabetic code (Garsia-Wachs)
+    within 8 bits for at most 256 counted symbols (12 above), else Shannon
+    lengths.  The reference zero-fills the output first; the kernel writes
+    every entry of it, so it is allocated without a fill."""
     if _ext is not None:
         return _ext.calculate_cdf(input, int(n_bins))
     if not input.is_cuda:
