@@ -1648,7 +1648,7 @@ bool contiguous(const lmc_tensor &t) {
 }
 
 void need_device(const lmc_tensor &t, const char *what) {
-  check(t.device >= 0, std::string(what) + " should be on the GPU");
+  check(t.device >= 0, std::string(what) + " is not a GPU tensor");
   check(contiguous(t), std::string(what) + " must be contiguous");
 }
 
@@ -1797,10 +1797,10 @@ int lmc_decode_fast_prefsum(const lmc_tensor *cdf_t,
     const lmc_tensor &ln = deref(lengths, "lengths");
     const lmc_tensor &o = deref(output, "output");
     // csrc/cachegen_kernels.cpp:78-88
-    check(cdf.device >= 0, "CDFs tensor should be on the GPU");
-    check(bs.device >= 0, "Bytestreams tensor should be on the GPU");
-    check(ln.device >= 0, "Lengths tensor should be on the GPU");
-    check(o.device >= 0, "Output tensor should be on the GPU");
+    check(cdf.device >= 0, "cdf is not a GPU tensor");
+    check(bs.device >= 0, "bytestreams is not a GPU tensor");
+    check(ln.device >= 0, "lengths is not a GPU tensor");
+    check(o.device >= 0, "output is not a GPU tensor");
     need_device(cdf, "cdf");
     need_device(bs, "bytestreams");
     need_device(ln, "lengths");

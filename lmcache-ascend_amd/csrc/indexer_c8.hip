@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(kC8Threads) indexer_c8_copy(C8Job job) {
 void check_state(const lmc_tensor &keys, const lmc_tensor *scales,
                  int64_t factor, const lmc_tensor *block_map) {
   check(keys.device >= 0 && (scales == nullptr || scales->device == keys.device),
-        "C8 destinations must share one GPU device");
+        "the C8 caches are on different GPUs");
   const bool quantized = keys.dtype == LMC_I8;
   check(quantized ? scales != nullptr && scales->dtype == LMC_F16
                   : scales == nullptr && (keys.dtype == LMC_F16 || keys.dtype == LMC_BF16),

@@ -174,7 +174,7 @@ void sparse_graph(const lmc_tensor &k, const lmc_tensor &pe, int64_t kH, int64_t
   check(sel.device >= 0 && slots.device == sel.device && counts.device == sel.device &&
             ptrs.device == sel.device && limits.device == sel.device &&
             k.device == sel.device && pe.device == sel.device,
-        "Graph transfer inputs must be on the same GPU");
+        "the graph transfer's tensors are on different GPUs");
   check(max_cores >= 0 && max_cores <= UINT32_MAX,
         "max_aiv_cores is negative or above the uint32 range");
   DeviceGuard guard(sel.device);

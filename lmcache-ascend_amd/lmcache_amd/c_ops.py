@@ -86,7 +86,7 @@ def _desc(t: torch.Tensor) -> _lib.LmcTensor:
     try:
         dt = _DTYPES[t.dtype]
     except KeyError:
-        raise RuntimeError(f"ScalarType not supported: {t.dtype}") from None
+        raise RuntimeError(f"no lmc_tensor dtype code for {t.dtype}") from None
     except AttributeError:
         raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}") from None
     if t.is_cuda:
