@@ -142,8 +142,11 @@ __device__ __forceinline__ void wave_sync_cdf() {
 }
 
 // LDS of cdf_tile_kernel: [staged symbols, later the compacted count lists]
-// [histogram [nb][64] u32] [count sums] [Garsia-Wachs flags] [present
-// symbols] [partial interval sums [4][64]] [rows [64][nb + 1] int16].
+// [histogram [nb][64] u32] [partial interval sums [4][64]] [count sums]
+// [Garsia-Wachs flags] [present symbols] [rows [64][nb + 1] int16].  The
+// partial sums' first row doubles as histogram row nb while the symbols are
+// counted: symbols >= nb are counted there, and the row is written before
+// it is read as partial sums.
 // The first area holds a staged piece (at most 256 x 64 bytes), the count
 // lists (nb <= 64 rows of 64 words) and the node-id mode's leaf sets (63
 // rows): 64 rows of 64 words whatever T and nb.
@@ -179,11 +182,21 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
   }
   wave_sync_cdf();
   typename It::V a[CAP];
+  uint32_t lw[CAP];
 #pragma unroll
   for (int i = 0; i < CAP; ++i) {
     const int pos = Q * i + g;
-    const uint32_t w = lst[(pos < nb ? pos : nb - 1) * 64];
-    a[i] = pos < m ? It::leaf(w, pos) : It::inf();
+    lw[i] = lst[(pos < nb ? pos : nb - 1) * 64];
+  }
+#pragma unroll
+  for (int i = 0; i < CAP; ++i) {
+    // The empty asm takes the loaded word as an operand, so the loads stay
+    // unconditional and back to back: otherwise the compiler moves each
+    // load into a branch on `pos < m` and waits for it there (16 serial
+    // LDS round trips in the one-lane mode).
+    asm volatile("" : "+v"(lw[i]));
+    const int pos = Q * i + g;
+    a[i] = pos < m ? It::leaf(lw[i], pos) : It::inf();
   }
   if constexpr (std::is_same<It, cggw::ItemId>::value) {
     // Leaf sets by id over the dead list: leaf j's at word j.
@@ -215,6 +228,12 @@ template <int kBins, bool kExact>
 __global__ void __launch_bounds__(kCdfThreads)
     cdf_tile_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
                     int16_t *__restrict__ out, int tiles, int vec_tile) {
+  // Wave priority: 1 outside the Garsia-Wachs steps, 0 during them.  A
+  // step wave issues VALU almost every cycle, and the SIMD arbiter prefers
+  // the oldest wave among equals, so without this the steps of an earlier
+  // block kept the later blocks' waves on the same SIMD from counting their
+  // symbols (their staging and histogram phase took up to 2x longer).
+  __builtin_amdgcn_s_setprio(1);
   if (kExact) nb = kBins;
   extern __shared__ uint32_t lds[];
   const int tid = static_cast<int>(threadIdx.x);
@@ -225,12 +244,13 @@ __global__ void __launch_bounds__(kCdfThreads)
   const int cnt = C - c0 < 64 ? C - c0 : 64;
   uint8_t *tile = reinterpret_cast<uint8_t *>(lds);
   uint32_t *hist = lds + cdf_stage_words(T, nb);
-  uint32_t *nsum = hist + nb * 64;   // per stream: symbol count
-  uint32_t *gwok = nsum + 64;        // per stream: Garsia-Wachs lengths taken
-  uint32_t *msum = gwok + 64;        // per stream: present symbols
-  uint32_t *psum = msum + 64;        // [wave][stream]: partial interval sums
-  int16_t *rows = reinterpret_cast<int16_t *>(psum + kCdfWaves * 64);
-  for (int i = tid; i < nb * 64 + 192; i += kCdfThreads) hist[i] = 0;
+  uint32_t *psum = hist + nb * 64;          // [wave][stream]: partial interval sums
+  uint32_t *nsum = psum + kCdfWaves * 64;   // per stream: symbol count
+  uint32_t *gwok = nsum + 64;               // per stream: Garsia-Wachs lengths taken
+  uint32_t *msum = gwok + 64;               // per stream: present symbols
+  int16_t *rows = reinterpret_cast<int16_t *>(msum + 64);
+  for (int i = tid; i < nb * 64; i += kCdfThreads) hist[i] = 0;
+  if (tid < 192) nsum[tid] = 0;
   for (int t0 = 0; t0 < T; t0 += kCdfPiece) {
     const int tc = T - t0 < kCdfPiece ? T - t0 : kCdfPiece;
     if (t0 > 0) __syncthreads();  // the previous piece has been counted
@@ -259,7 +279,9 @@ __global__ void __launch_bounds__(kCdfThreads)
     const int tb = q * Tq < tc ? q * Tq : tc;
     const int te = tb + Tq < tc ? tb + Tq : tc;
     if (lane < cnt && tb < te) {
-      // Symbols that are not counted add 0 to row 0 (no branch per symbol).
+      // Symbols >= nb (and the padding of a partial batch) are counted in
+      // row nb, the partial sums' first row, which no count read sees: two
+      // VALU operations per symbol (the row, then the address) and no branch.
       const int tq = te - tb;
       const uint8_t *scol = tile + tb * 64 + lane;
       for (int u0 = 0; u0 < tq; u0 += kBatch) {
@@ -272,10 +294,8 @@ __global__ void __launch_bounds__(kCdfThreads)
           for (int i = 0; i < kBatch; ++i) sym[i] = u0 + i < tq ? scol[(u0 + i) * 64] : 0xFFu;
         }
 #pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          const bool ok = sym[i] < static_cast<uint32_t>(nb);
-          atomicAdd(&hist[(ok ? sym[i] : 0u) * 64 + lane], ok ? 1u : 0u);
-        }
+        for (int i = 0; i < kBatch; ++i)
+          atomicAdd(&hist[min(sym[i], static_cast<uint32_t>(nb)) * 64 + lane], 1u);
       }
     }
   }
@@ -316,6 +336,7 @@ __global__ void __launch_bounds__(kCdfThreads)
     const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 48));
     const int mm = static_cast<int>(max(max(r0, r1), max(r2, r3)));
     uint32_t *lists = lds;  // the staged symbols are dead
+    __builtin_amdgcn_s_setprio(0);
     if (mm >= 2) {
       if (mm <= 16 && T < 65536) {
         if (q == static_cast<int>(blockIdx.x % kCdfWaves))
@@ -330,6 +351,7 @@ __global__ void __launch_bounds__(kCdfThreads)
     }
   }
   __syncthreads();
+  __builtin_amdgcn_s_setprio(1);
   // Lengths and interval assignment, spread over the waves: wave q takes
   // symbols [j0, j1) of every stream (lane = stream).  A Garsia-Wachs stream
   // keeps its tree's depths; the others (one present symbol, no counted
@@ -433,17 +455,20 @@ __global__ void __launch_bounds__(kCdfThreads)
       len[s] = s < nb ? v >> kLenShift : 0u;
     }
     int16_t *row = rows + lane * (nb + 1);
-    uint32_t pos = 0;
+    // r is the running base with bit 16 set, so its lowest set bit is the
+    // base's alignment (0x10000 for base 0, above every width); the width
+    // taken is min(2^(16 - length), that bit), and the length follows from
+    // it.  The chain from one symbol to the next is four operations.
+    uint32_t r = 1u << kPrec;
 #pragma unroll
     for (int s = 0; s < kBins; ++s) {
       if (s < nb) {
         const uint32_t x0 = len[s];
         const uint32_t w0 = x0 ? 1u << (kPrec - x0) : 0u;
-        const uint32_t low = pos & (0u - pos);  // lowest set bit (0 when pos == 0)
-        const bool shrink = low != 0 && low < w0;
-        const uint32_t x = shrink ? x0 + static_cast<uint32_t>(__builtin_clz(low) - __builtin_clz(w0)) : x0;
-        row[s] = static_cast<int16_t>(static_cast<uint16_t>((pos | x) & 0xFFFFu));
-        pos += shrink ? low : w0;
+        const uint32_t w = min(w0, r & (0u - r));
+        const uint32_t x = x0 ? static_cast<uint32_t>(__builtin_clz(w)) - (31u - kPrec) : 0u;
+        row[s] = static_cast<int16_t>(static_cast<uint16_t>((r | x) & 0xFFFFu));
+        r += w;
       }
     }
   }

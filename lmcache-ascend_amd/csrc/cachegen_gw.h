@@ -110,6 +110,70 @@ __device__ __forceinline__ typename It::V quad_or(typename It::V v) {
   return It::bor(v, qp<kRot2>(v));
 }
 
+// Per-slot conditions as VGPR words.  A compare writes an SGPR lane mask
+// that a select may read only two wait states later, and the list update
+// is a run of compare-select pairs on one mask register, so each pair
+// waited; a slot's condition is instead bit i of a per-lane word, spread
+// to a lane mask by a bit-field extract and applied by v_bfi_b32.
+// All ones where bit i of `bits` is set (i a constant after unrolling).
+__device__ __forceinline__ uint32_t bit_mask(uint32_t bits, int i) {
+  return static_cast<uint32_t>(static_cast<int32_t>(bits << (31 - i)) >> 31);
+}
+// Bitwise m ? x : y.  Written as asm: the compiler turns the C form of a
+// select on a sign mask back into a compare and an SGPR select.
+__device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t x, uint32_t y) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(x), "v"(y));
+  return r;
+}
+// Bit length of x: 0 for 0, else 1 + the index of the highest set bit.
+__device__ __forceinline__ int bit_length(uint32_t x) { return 32 - static_cast<int>(__builtin_clzg(x, 32)); }
+
+// The re-insertion point and the new list of a step for 32-bit items
+// whose weight is the top 16 bits (Item16, ItemId): `kg` = k - g, `sum`
+// the combined item.  Slot i holds position Q * i + g.  The point is
+// right after the last position before k whose weight is >= sum's (0
+// when none is): the sign bits of weight - sw, one per slot, are gathered
+// into a word by funnel shifts, and the last slot that qualifies is the
+// word's bit length.  The new list keeps [0, p), puts sum at p, takes
+// (p, k] from one position to the left and the rest from one position to
+// the right; each slot's three choices are selects on bits of per-lane
+// threshold words.
+template <int Q, int S, int CAP>
+__device__ __forceinline__ void reinsert32(uint32_t (&a)[CAP], const uint32_t (&dn1)[S], const uint32_t (&up1)[S],
+                                           int g, int kg, uint32_t sum) {
+  static_assert(Q == 1 || Q == 4, "lanes per stream");
+  constexpr int kLog = Q == 4 ? 2 : 0;
+  const uint32_t sw = sum >> 16;
+  uint32_t light = 0;  // bit i: slot i's weight is below sw
+#pragma unroll
+  for (int i = S - 1; i >= 0; --i) light = __builtin_amdgcn_alignbit(light, (a[i] >> 16) - sw, 31);
+  // Slots before k: Q * i < kg, i < ceil(kg / Q) (kg >= 1 - Q).
+  const uint32_t before_k = (1u << ((kg + Q - 1) >> kLog)) - 1u;
+  const int bl = bit_length(~light & before_k);  // the last such slot + 1
+  int p;
+  if constexpr (Q == 1) {
+    p = bl;
+  } else {
+    // Position 4 (bl - 1) + g + 1 of the lane's last heavy slot, or 0.
+    const int pq = max(4 * bl + g - 3, 0);
+    p = static_cast<int>(quad_max(static_cast<uint32_t>(pq)));
+  }
+  const int pg = p - g;
+  const uint32_t to_left = (1u << ((kg + Q) >> kLog)) - 1u;   // Q * i <= kg
+  const uint32_t keep = (1u << ((pg + Q - 1) >> kLog)) - 1u;  // Q * i < pg
+  const uint32_t at_p = ((1u << ((pg + Q) >> kLog)) - 1u) ^ keep;  // Q * i == pg
+  uint32_t na[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    uint32_t v = bsel(bit_mask(to_left, i), dn1[i], up1[i]);
+    v = bsel(bit_mask(at_p, i), sum, v);
+    na[i] = bsel(bit_mask(keep, i), a[i], v);
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) a[i] = na[i];
+}
+
 // Bit-sliced depth counters: bit j of d0..d3 is leaf j's depth (mod 16),
 // bit j of ovf is set once it reaches 16.
 template <class L>
@@ -193,36 +257,40 @@ __device__ __forceinline__ void step(typename It::V (&a)[CAP], int g, bool activ
     k = static_cast<int>(quad_min(kq));
     sum = quad_or<It>(kq == static_cast<uint32_t>(k) ? sloc : It::zero());
   }
-  // Re-insertion point: right after the last position before k whose
-  // weight is >= the combined weight (0 when none is).
-  const uint32_t sw = It::weight(sum);
   const int kg = k - g;
-  int pslot = -1;
-#pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const bool c = Q * i < kg && It::weight(a[i]) >= sw;
-    pslot = c ? i : pslot;
-  }
-  int p;
-  if constexpr (Q == 1) {
-    p = pslot + 1;
+  if constexpr (std::is_same<V, uint32_t>::value) {
+    reinsert32<Q, S, CAP>(a, dn1, up1, g, kg, sum);
   } else {
-    const uint32_t pq = pslot >= 0 ? static_cast<uint32_t>(Q * pslot + g + 1) : 0u;
-    p = static_cast<int>(quad_max(pq));
-  }
-  // New list: [0, p) kept, the combined item at p, (p, k] from one position
-  // to the left, the rest from one position to the right (k and k + 1 are
-  // gone).
-  const int pg = p - g;
-  V na[S];
+    // Re-insertion point: right after the last position before k whose
+    // weight is >= the combined weight (0 when none is).
+    const uint32_t sw = It::weight(sum);
+    int pslot = -1;
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    V v = Q * i <= kg ? dn1[i] : up1[i];
-    v = Q * i == pg ? sum : v;
-    na[i] = Q * i < pg ? a[i] : v;
-  }
+    for (int i = 0; i < S; ++i) {
+      const bool c = Q * i < kg && It::weight(a[i]) >= sw;
+      pslot = c ? i : pslot;
+    }
+    int p;
+    if constexpr (Q == 1) {
+      p = pslot + 1;
+    } else {
+      const uint32_t pq = pslot >= 0 ? static_cast<uint32_t>(Q * pslot + g + 1) : 0u;
+      p = static_cast<int>(quad_max(pq));
+    }
+    // New list: [0, p) kept, the combined item at p, (p, k] from one
+    // position to the left, the rest from one position to the right (k and
+    // k + 1 are gone).
+    const int pg = p - g;
+    V na[S];
 #pragma unroll
-  for (int i = 0; i < S; ++i) a[i] = na[i];
+    for (int i = 0; i < S; ++i) {
+      V v = Q * i <= kg ? dn1[i] : up1[i];
+      v = Q * i == pg ? sum : v;
+      na[i] = Q * i < pg ? a[i] : v;
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i) a[i] = na[i];
+  }
   dep.add(active ? It::leaves(sum) : typename It::L(0));
 }
 
@@ -295,27 +363,7 @@ __device__ __forceinline__ void step_ids(uint32_t (&a)[CAP], int g, bool active,
   const uint32_t sy = sets[iy * 64];
   const uint32_t sw = It::weight(x) + It::weight(y);
   const uint32_t sum = (sw << 16) | static_cast<uint32_t>(32 + t);
-  // Re-insertion point: right after the last position before k whose
-  // weight is >= the combined weight (0 when none is).
-  const int kg = k - g;
-  int pslot = -1;
-#pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const bool c = Q * i < kg && It::weight(a[i]) >= sw;
-    pslot = c ? i : pslot;
-  }
-  const uint32_t pq = pslot >= 0 ? static_cast<uint32_t>(Q * pslot + g + 1) : 0u;
-  const int p = static_cast<int>(quad_max(pq));
-  const int pg = p - g;
-  uint32_t na[S];
-#pragma unroll
-  for (int i = 0; i < S; ++i) {
-    uint32_t v = Q * i <= kg ? dn1[i] : up1[i];
-    v = Q * i == pg ? sum : v;
-    na[i] = Q * i < pg ? a[i] : v;
-  }
-#pragma unroll
-  for (int i = 0; i < S; ++i) a[i] = na[i];
+  reinsert32<Q, S, CAP>(a, dn1, up1, g, k - g, sum);
   const uint32_t set = sx | sy;
   sets[(32 + t) * 64] = set;
   dep.add(active ? set : 0u);
