@@ -237,7 +237,9 @@ __global__ void __launch_bounds__(kCdfThreads)
   if (kExact) nb = kBins;
   extern __shared__ uint32_t lds[];
   const int tid = static_cast<int>(threadIdx.x);
-  const int q = tid / 64;
+  // The wave index, read as a scalar: every per-wave bound below (a wave's
+  // symbol share, the wave that runs the one-lane steps) is then uniform.
+  const int q = __builtin_amdgcn_readfirstlane(tid / 64);
   const int lane = tid % 64;
   const int l = blockIdx.x / tiles;
   const int c0 = (blockIdx.x % tiles) * 64;
@@ -312,7 +314,7 @@ __global__ void __launch_bounds__(kCdfThreads)
     for (int k = 0; k < kS; ++k) {
       const uint32_t c = (k < share && j0 + k < j1) ? hist[(j0 + k) * 64 + lane] : 0u;
       part += c;
-      present += c != 0 ? 1u : 0u;
+      present += min(c, 1u);
     }
     if (lane < cnt && part) {
       atomicAdd(nsum + lane, part);
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(kCdfThreads)
   const bool gw = gwok[lane] != 0;
   {
     const uint32_t n = nsum[lane];
-    const int ln = 31 - __builtin_clz(n | 1u);
+    const int ln31 = -__builtin_clz(n | 1u);  // floor(log2 n) - 31
     // A Garsia-Wachs stream's depths by leaf (the leaf of symbol s is the
     // number of present symbols below it).
     const uint32_t *dcol = lds + lane;
@@ -374,34 +376,50 @@ __global__ void __launch_bounds__(kCdfThreads)
     for (int k = 0; k < 4; ++k)
       dsl[k] = static_cast<uint64_t>(dcol[k * 64]) | (static_cast<uint64_t>(dcol[(4 + k) * 64]) << 32);
     const uint64_t pres = static_cast<uint64_t>(dcol[8 * 64]) | (static_cast<uint64_t>(dcol[9 * 64]) << 32);
+    // The wave's counts (plain counts: no length is stored yet), all read
+    // before the first is used; the empty asm keeps each read unconditional
+    // (the compiler would otherwise move it into a branch and wait there).
+    uint32_t cv[kS];
+#pragma unroll
+    for (int k = 0; k < kS; ++k) cv[k] = hist[min(j0 + k, nb - 1) * 64 + lane];
+#pragma unroll
+    for (int k = 0; k < kS; ++k) asm volatile("" : "+v"(cv[k]));
     uint32_t len[kS];
     uint32_t own = 0;
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
-      const bool in_range = k < share && j0 + k < j1;
+      const bool in_range = kExact || (k < share && j0 + k < j1);  // uniform
       const int s = in_range ? j0 + k : 0;
-      const uint32_t v = in_range ? hist[s * 64 + lane] : 0u;
-      const uint32_t cs = v & kCountMask;
-      uint32_t x = static_cast<uint32_t>(ln - (31 - __builtin_clz(cs | 1u)));
-      x += (static_cast<uint64_t>(cs) << x) < n ? 1u : 0u;
-      x = x < 1 ? 1 : (x > kMaxLen ? kMaxLen : x);
+      const uint32_t cs = in_range ? cv[k] : 0u;
+      // The Shannon length: the smallest x with cs << x >= n, which is
+      // x0 = floor(log2 n) - floor(log2 cs) or x0 + 1.  For cs >= 1,
+      // cs << x0 < 2^(floor(log2 n) + 1) <= 2^26, so the test is a 32-bit
+      // subtraction's sign.
+      int x = ln31 + static_cast<int>(__builtin_clz(cs | 1u));  // x0
+      x += static_cast<int>(((cs << x) - n) >> 31);
+      x = min(max(x, 1), kMaxLen);
       const int j = kBins <= 32 ? __builtin_popcount(static_cast<uint32_t>(pres) & ((1u << s) - 1u))
                                 : __builtin_popcountll(pres & ((1ull << s) - 1ull));
       uint32_t depth;
       if constexpr (kBins <= 32) {
-        const int jj = j & 31;
-        depth = ((static_cast<uint32_t>(dsl[0]) >> jj) & 1u) | (((static_cast<uint32_t>(dsl[1]) >> jj) & 1u) << 1) |
-                (((static_cast<uint32_t>(dsl[2]) >> jj) & 1u) << 2) |
-                (((static_cast<uint32_t>(dsl[3]) >> jj) & 1u) << 3);
+        const uint32_t jj = static_cast<uint32_t>(j) & 31u;
+        depth = __builtin_amdgcn_ubfe(static_cast<uint32_t>(dsl[0]), jj, 1u) |
+                (__builtin_amdgcn_ubfe(static_cast<uint32_t>(dsl[1]), jj, 1u) << 1) |
+                (__builtin_amdgcn_ubfe(static_cast<uint32_t>(dsl[2]), jj, 1u) << 2) |
+                (__builtin_amdgcn_ubfe(static_cast<uint32_t>(dsl[3]), jj, 1u) << 3);
       } else {
         const int jj = j & 63;
         depth = static_cast<uint32_t>(((dsl[0] >> jj) & 1u) | (((dsl[1] >> jj) & 1u) << 1) |
                                       (((dsl[2] >> jj) & 1u) << 2) | (((dsl[3] >> jj) & 1u) << 3));
       }
-      x = cs ? (gw ? depth : x) : 0u;
-      len[k] = x;
-      own += x ? 1u << (kPrec - x) : 0u;
-      if (in_range && !gw) hist[s * 64 + lane] = (x << kLenShift) | cs;
+      // Both lengths are computed for every symbol (no branch on cs).
+      uint32_t xs = static_cast<uint32_t>(x);
+      asm volatile("" : "+v"(xs), "+v"(depth));
+      const uint32_t xl = cs ? (gw ? depth : xs) : 0u;
+      len[k] = xl;
+      own += 0x8000u >> ((xl - 1u) & 31u);  // 2^(16 - xl), 0 for xl = 0
+      // Every lane stores; only the Shannon streams' words are read again.
+      if (in_range) hist[s * 64 + lane] = (xl << kLenShift) | cs;
     }
     psum[q * 64 + lane] = own;
     __syncthreads();
