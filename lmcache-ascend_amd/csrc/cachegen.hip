@@ -169,16 +169,19 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
   // symbol's count is written at the next free position (m <= s < nb), so
   // an absent one is overwritten by the next present one or lies past the
   // list; the lanes of a group write the same words.  No branches.
-  uint64_t pres = 0;
+  // The histogram holds plain counts here (lengths are stored later).
+  using PM = typename std::conditional<(kBins <= 32), uint32_t, uint64_t>::type;
+  PM pres = 0;
   int m = 0;
   uint32_t cs[kBins];
 #pragma unroll
-  for (int s = 0; s < kBins; ++s) cs[s] = s < nb ? col[s * 64] & kCountMask : 0u;
+  for (int s = 0; s < kBins; ++s) cs[s] = s < nb ? col[s * 64] : 0u;
 #pragma unroll
   for (int s = 0; s < kBins; ++s) {
     if (s < nb) lst[m * 64] = cs[s];
-    pres |= static_cast<uint64_t>(cs[s] != 0) << s;
-    m += cs[s] != 0 ? 1 : 0;
+    const uint32_t here = min(cs[s], 1u);  // present: no compare, no SGPR mask
+    pres |= static_cast<PM>(here) << s;
+    m += static_cast<int>(here);
   }
   wave_sync_cdf();
   typename It::V a[CAP];
@@ -218,7 +221,7 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
     lst[(4 + k) * 64] = static_cast<uint32_t>(static_cast<uint64_t>(d[k]) >> 32);
   }
   lst[8 * 64] = static_cast<uint32_t>(pres);
-  lst[9 * 64] = static_cast<uint32_t>(pres >> 32);
+  lst[9 * 64] = static_cast<uint32_t>(static_cast<uint64_t>(pres) >> 32);
   gwok[stream] = 1u;
 }
 
@@ -228,11 +231,17 @@ template <int kBins, bool kExact>
 __global__ void __launch_bounds__(kCdfThreads)
     cdf_tile_kernel(const uint8_t *__restrict__ in, int T, int C, int nb,
                     int16_t *__restrict__ out, int tiles, int vec_tile) {
-  // Wave priority: 1 outside the Garsia-Wachs steps, 0 during them.  A
-  // step wave issues VALU almost every cycle, and the SIMD arbiter prefers
-  // the oldest wave among equals, so without this the steps of an earlier
-  // block kept the later blocks' waves on the same SIMD from counting their
-  // symbols (their staging and histogram phase took up to 2x longer).
+  // Wave priority: 1, and 0 for a wave making the one-lane Garsia-Wachs
+  // steps.  A step wave issues VALU almost every cycle and the SIMD arbiter
+  // prefers the oldest wave among equals: with every wave at one priority,
+  // the steps of an earlier block kept the later blocks' waves on the same
+  // SIMD from counting their symbols (that phase took up to 2x longer).  The
+  // one-lane steps (at most 16 present symbols) are the shortest chain of
+  // the kernel, so they yield; the quad steps of the blocks with up to 32
+  // present symbols, the longest chain, keep priority 1.  Measured on a
+  // 32 x 256 x 1024 K+V chunk in a standalone build of this kernel: one
+  // priority for every wave 26.1 us; priority 0 for both kinds of steps
+  // 23.6 (23.3 once the lengths phase lost its branches); this 22.6.
   __builtin_amdgcn_s_setprio(1);
   if (kExact) nb = kBins;
   extern __shared__ uint32_t lds[];
@@ -338,9 +347,9 @@ __global__ void __launch_bounds__(kCdfThreads)
     const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m_max), 48));
     const int mm = static_cast<int>(max(max(r0, r1), max(r2, r3)));
     uint32_t *lists = lds;  // the staged symbols are dead
-    __builtin_amdgcn_s_setprio(0);
     if (mm >= 2) {
       if (mm <= 16 && T < 65536) {
+        __builtin_amdgcn_s_setprio(0);
         if (q == static_cast<int>(blockIdx.x % kCdfWaves))
           gw_lengths<1, 16, cggw::Item16, kBins>(hist, lists, gwok, nsum, nb, lane, 0, mm);
       } else if (mm <= 32 && T < 65536) {
@@ -430,9 +439,9 @@ __global__ void __launch_bounds__(kCdfThreads)
       for (int w = 0; w < kCdfWaves - 1; ++w) pos += w < q ? psum[w * 64 + lane] : 0u;
 #pragma unroll
       for (int k = 0; k < kS; ++k) {
-        if (k < share && j0 + k < j1) {
+        if (kExact || (k < share && j0 + k < j1)) {
           row[j0 + k] = static_cast<int16_t>(static_cast<uint16_t>((pos | len[k]) & 0xFFFFu));
-          pos += len[k] ? 1u << (kPrec - len[k]) : 0u;
+          pos += 0x8000u >> ((len[k] - 1u) & 31u);  // 2^(16 - len), 0 for len 0
         }
       }
     }
