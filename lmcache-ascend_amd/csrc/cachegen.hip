@@ -186,9 +186,13 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
   wave_sync_cdf();
   typename It::V a[CAP];
   uint32_t lw[CAP];
+  // List position of slot i: lane-major (g CAP + i) for the node-id quads,
+  // interleaved (Q i + g) otherwise.
+  constexpr bool kLaneMajor = std::is_same<It, cggw::ItemId>::value && Q == 4;
+  auto position = [g](int i) { return kLaneMajor ? g * CAP + i : Q * i + g; };
 #pragma unroll
   for (int i = 0; i < CAP; ++i) {
-    const int pos = Q * i + g;
+    const int pos = position(i);
     lw[i] = lst[(pos < nb ? pos : nb - 1) * 64];
   }
 #pragma unroll
@@ -198,13 +202,13 @@ __device__ __forceinline__ void gw_lengths(uint32_t *hist, uint32_t *lists, uint
     // load into a branch on `pos < m` and waits for it there (16 serial
     // LDS round trips in the one-lane mode).
     asm volatile("" : "+v"(lw[i]));
-    const int pos = Q * i + g;
+    const int pos = position(i);
     a[i] = pos < m ? It::leaf(lw[i], pos) : It::inf();
   }
   if constexpr (std::is_same<It, cggw::ItemId>::value) {
     // Leaf sets by id over the dead list: leaf j's at word j.
 #pragma unroll
-    for (int i = 0; i < CAP; ++i) lst[(Q * i + g) * 64] = 1u << (Q * i + g);
+    for (int i = 0; i < CAP; ++i) lst[position(i) * 64] = 1u << position(i);
   }
   cggw::Depths<typename It::L> dep;
   cggw::run<Q, CAP, It>(a, g, m, m_max, dep, lst);

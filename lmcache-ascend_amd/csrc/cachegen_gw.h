@@ -96,6 +96,17 @@ __device__ __forceinline__ Item64::V qp(Item64::V v) {
   return Item64::V{qp<CTRL>(v.m), qp<CTRL>(v.w)};
 }
 
+// A quad permutation whose result is then selected per lane.  The empty
+// asm makes every lane execute the permutation: the compiler would
+// otherwise fold the select into the permutation under a reduced exec
+// mask, and a permutation reads 0 from the lanes that mask turns off.
+template <int CTRL>
+__device__ __forceinline__ uint32_t qps(uint32_t v) {
+  uint32_t r = qp<CTRL>(v);
+  asm volatile("" : "+v"(r));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t quad_min(uint32_t v) {
   v = min(v, qp<kSwap>(v));
   return min(v, qp<kRot2>(v));
@@ -326,9 +337,9 @@ __device__ __forceinline__ void step_ids(uint32_t (&a)[CAP], int g, bool active,
     uint32_t r1[S], r2[S], r3[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      r1[i] = qp<kRot1>(a[i]);
-      r3[i] = qp<kRot3>(a[i]);
-      r2[i] = qp<kRot2>(a[i]);
+      r1[i] = qps<kRot1>(a[i]);
+      r3[i] = qps<kRot3>(a[i]);
+      r2[i] = qps<kRot2>(a[i]);
     }
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -388,6 +399,155 @@ __device__ __forceinline__ void phases(typename It::V (&a)[CAP], int g, int m_la
   }
 }
 
+// Lane-major quads for ItemId.  With S slots a lane, list position q is
+// slot q % S of lane q / S, so the neighbours at q - 1, q + 1 and q + 2 are
+// the lane's own registers except across a lane boundary, where three quad
+// permutations a step bring them (against three permutations and three
+// selects a slot in the interleaved layout).  When the list has shrunk by
+// four positions, the items move to the layout with one slot fewer
+// (repack_lm); with one slot both layouts are the same.
+
+// The re-insertion point and the new list in the lane-major layout: `base`
+// is this lane's first position (g S).
+template <int S, int CAP>
+__device__ __forceinline__ void reinsert_lm(uint32_t (&a)[CAP], const uint32_t (&dn1)[S], const uint32_t (&up1)[S],
+                                            int base, int k, uint32_t sum) {
+  const uint32_t sw = sum >> 16;
+  uint32_t light = 0;  // bit i: slot i's weight is below sw
+#pragma unroll
+  for (int i = S - 1; i >= 0; --i) light = __builtin_amdgcn_alignbit(light, (a[i] >> 16) - sw, 31);
+  const int kk = k - base;  // k's slot in this lane (may lie outside [0, S))
+  const uint32_t before_k = (1u << min(max(kk, 0), S)) - 1u;
+  const int bl = bit_length(~light & before_k);  // the lane's last heavy slot before k, + 1
+  // Its position + 1, or 0 when the lane has none (bl << 6 exceeds every position).
+  const int pq = min(base + bl, bl << 6);
+  const int pp = static_cast<int>(quad_max(static_cast<uint32_t>(pq))) - base;
+  const uint32_t to_left = (1u << min(max(kk + 1, 0), S)) - 1u;  // position <= k
+  const uint32_t keep = (1u << min(max(pp, 0), S)) - 1u;         // position < p
+  const uint32_t at_p = ((1u << min(max(pp + 1, 0), S)) - 1u) ^ keep;
+  uint32_t na[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    uint32_t v = bsel(bit_mask(to_left, i), dn1[i], up1[i]);
+    v = bsel(bit_mask(at_p, i), sum, v);
+    na[i] = bsel(bit_mask(keep, i), a[i], v);
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) a[i] = na[i];
+}
+
+// One combination step in the lane-major layout (S >= 2); the rest as in
+// step_ids.
+template <int S, int CAP>
+__device__ __forceinline__ void step_lm(uint32_t (&a)[CAP], int g, bool active, int t, int tmax, uint32_t *sets,
+                                        Depths<uint32_t> &dep) {
+  using It = ItemId;
+  static_assert(S >= 2 && S <= CAP, "slots");
+  // Lane g + 1's first two items (positions past the list for lane 3) and
+  // lane g - 1's last (never taken by lane 0: position -1 is never moved).
+  const bool last = g == 3;
+  // (Each permutation is its own statement: an arm of ?: runs only where
+  // it is chosen.)
+  const uint32_t r0 = qps<kRot1>(a[0]);
+  const uint32_t r1 = qps<kRot1>(a[1]);
+  const uint32_t pv = qps<kRot3>(a[S - 1]);
+  const uint32_t nx0 = last ? It::inf() : r0;
+  const uint32_t nx1 = last ? It::inf() : r1;
+  uint32_t up1[S], dn1[S], up2[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    up1[i] = i + 1 < S ? a[i + 1 < S ? i + 1 : 0] : nx0;
+    dn1[i] = i > 0 ? a[i > 0 ? i - 1 : 0] : pv;
+    up2[i] = i + 2 < S ? a[i + 2 < S ? i + 2 : 0] : (i + 2 == S ? nx0 : nx1);
+  }
+  int kslot = -1;
+  uint32_t xs = 0, ys = 0;
+#pragma unroll
+  for (int i = S - 1; i >= 0; --i) {
+    const bool c = It::weight(a[i]) <= It::weight(up2[i]);
+    kslot = c ? i : kslot;
+    xs = c ? a[i] : xs;
+    ys = c ? up1[i] : ys;
+  }
+  const int base = g * S;
+  const uint32_t kq = kslot >= 0 ? static_cast<uint32_t>(base + kslot) : 0x3FFu;
+  const int k = static_cast<int>(quad_min(kq));
+  const bool own = kq == static_cast<uint32_t>(k);
+  const uint32_t x = quad_or<Item16>(own ? xs : 0u);
+  const uint32_t y = quad_or<Item16>(own ? ys : 0u);
+  const uint32_t top = static_cast<uint32_t>(32 + tmax);
+  const uint32_t ix = min(x & 0xFFFFu, top), iy = min(y & 0xFFFFu, top);
+  const uint32_t sx = sets[ix * 64];
+  const uint32_t sy = sets[iy * 64];
+  const uint32_t sw = It::weight(x) + It::weight(y);
+  const uint32_t sum = (sw << 16) | static_cast<uint32_t>(32 + t);
+  reinsert_lm<S, CAP>(a, dn1, up1, base, k, sum);
+  const uint32_t set = sx | sy;
+  sets[(32 + t) * 64] = set;
+  dep.add(active ? set : 0u);
+}
+
+// Moves the lane-major layout from S slots a lane to S - 1 (S >= 3): new
+// slot i of lane g is position g (S - 1) + i, which is the lane's own slot
+// i - g when i >= g and otherwise slot S - g + i of lane g - 1 (S >= 3
+// keeps every such position within one lane to the left).
+template <int S, int CAP>
+__device__ __forceinline__ void repack_lm(uint32_t (&a)[CAP], int g) {
+  static_assert(S >= 3 && S <= CAP, "slots");
+  uint32_t na[S - 1];
+#pragma unroll
+  for (int i = 0; i < S - 1; ++i) {
+    // Own slot i - g (an index below 0 is not taken).
+    uint32_t v = a[i];
+    v = g == 1 ? a[i >= 1 ? i - 1 : 0] : v;
+    v = g == 2 ? a[i >= 2 ? i - 2 : 0] : v;
+    v = g == 3 ? a[i >= 3 ? i - 3 : 0] : v;
+    if (i < 3) {
+      // Lane h sends its slot S - 1 - h + i to lane h + 1, which takes it
+      // when i < h + 1 (lanes h < i send a slot nobody takes).
+      uint32_t send = a[S - 1];
+      send = g == 1 && i <= 1 ? a[S - 2 + i] : send;
+      send = g == 2 && i <= 2 ? a[S - 3 + i] : send;
+      const uint32_t recv = qps<kRot3>(send);
+      v = i < g ? recv : v;
+    }
+    na[i] = v;
+  }
+#pragma unroll
+  for (int i = 0; i < S - 1; ++i) a[i] = na[i];
+}
+
+// From two slots a lane to one: lane g takes slot g & 1 of lane g >> 1.
+template <int CAP>
+__device__ __forceinline__ void repack_lm_2to1(uint32_t (&a)[CAP], int g) {
+  constexpr int kHalf = 0x50;  // quad permutation [0, 0, 1, 1]
+  const uint32_t s0 = qps<kHalf>(a[0]);
+  const uint32_t s1 = qps<kHalf>(a[1]);
+  a[0] = (g & 1) ? s1 : s0;
+}
+
+// Lane-major phases: steps while the wave's longest list has more than
+// 4 (S - 1) items, then the layout with one slot fewer; from one slot on,
+// the interleaved steps (the same layout).
+template <int S, int CAP>
+__device__ __forceinline__ void phases_lm(uint32_t (&a)[CAP], int g, int m_lane, int &M, int &t, int tmax,
+                                          Depths<uint32_t> &dep, uint32_t *sets) {
+  if constexpr (S >= 2) {
+    while (M > 4 * (S - 1)) {
+      step_lm<S, CAP>(a, g, t < m_lane - 1, t, tmax, sets, dep);
+      --M;
+      ++t;
+    }
+    if constexpr (S >= 3)
+      repack_lm<S, CAP>(a, g);
+    else
+      repack_lm_2to1<CAP>(a, g);
+    phases_lm<S - 1, CAP>(a, g, m_lane, M, t, tmax, dep, sets);
+  } else {
+    phases<4, 1, CAP, ItemId>(a, g, m_lane, M, t, tmax, dep, sets);
+  }
+}
+
 // Leaf depths of one stream's Garsia-Wachs tree, its first m_lane items in
 // a[] (the rest padding); m_max: the longest list of the wave, uniform.
 // `sets`: for ItemId, the stream's LDS column of leaf sets by id (the
@@ -398,7 +558,10 @@ __device__ __forceinline__ void run(typename It::V (&a)[CAP], int g, int m_lane,
                                     Depths<typename It::L> &dep, uint32_t *sets = nullptr) {
   int M = __builtin_amdgcn_readfirstlane(m_max);
   int t = 0;
-  phases<Q, CAP, CAP, It>(a, g, m_lane, M, t, M - 2, dep, sets);
+  if constexpr (std::is_same<It, ItemId>::value && Q == 4)
+    phases_lm<CAP, CAP>(a, g, m_lane, M, t, M - 2, dep, sets);
+  else
+    phases<Q, CAP, CAP, It>(a, g, m_lane, M, t, M - 2, dep, sets);
 }
 
 }  // namespace cggw
