@@ -130,6 +130,14 @@ __device__ __forceinline__ typename It::V quad_or(typename It::V v) {
 __device__ __forceinline__ uint32_t bit_mask(uint32_t bits, int i) {
   return static_cast<uint32_t>(static_cast<int32_t>(bits << (31 - i)) >> 31);
 }
+// The same as one v_bfe_i32 written as asm, for words that are shifts of
+// all ones, whose extract the compiler otherwise rewrites into two shifts
+// per slot.
+__device__ __forceinline__ uint32_t bit_mask1(uint32_t bits, int i) {
+  uint32_t r;
+  asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(r) : "v"(bits), "i"(i));
+  return r;
+}
 // Bitwise m ? x : y.  Written as asm: the compiler turns the C form of a
 // select on a sign mask back into a compare and an SGPR select.
 __device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t x, uint32_t y) {
@@ -412,25 +420,30 @@ __device__ __forceinline__ void phases(typename It::V (&a)[CAP], int g, int m_la
 template <int S, int CAP>
 __device__ __forceinline__ void reinsert_lm(uint32_t (&a)[CAP], const uint32_t (&dn1)[S], const uint32_t (&up1)[S],
                                             int base, int k, uint32_t sum) {
+  // Positions are below 4 S <= 32 and k <= 4 S - 2, so every shift below
+  // is at most 31; the words are suffixes (bit i set for slots at or after
+  // a bound), and bits at or above S are never read as slots.
+  static_assert(S >= 1 && 4 * S <= 32, "slots");
   const uint32_t sw = sum >> 16;
-  uint32_t light = 0;  // bit i: slot i's weight is below sw
+  uint32_t light = ~0u;  // bit i < S: slot i's weight is below sw; above S: set
 #pragma unroll
   for (int i = S - 1; i >= 0; --i) light = __builtin_amdgcn_alignbit(light, (a[i] >> 16) - sw, 31);
   const int kk = k - base;  // k's slot in this lane (may lie outside [0, S))
-  const uint32_t before_k = (1u << min(max(kk, 0), S)) - 1u;
-  const int bl = bit_length(~light & before_k);  // the lane's last heavy slot before k, + 1
+  const uint32_t from_k = ~0u << max(kk, 0);
+  const int bl = bit_length(~(light | from_k));  // the lane's last heavy slot before k, + 1
   // Its position + 1, or 0 when the lane has none (bl << 6 exceeds every position).
   const int pq = min(base + bl, bl << 6);
   const int pp = static_cast<int>(quad_max(static_cast<uint32_t>(pq))) - base;
-  const uint32_t to_left = (1u << min(max(kk + 1, 0), S)) - 1u;  // position <= k
-  const uint32_t keep = (1u << min(max(pp, 0), S)) - 1u;         // position < p
-  const uint32_t at_p = ((1u << min(max(pp + 1, 0), S)) - 1u) ^ keep;
+  const uint32_t right = ~0u << max(kk + 1, 0);  // positions after k
+  const uint32_t from_p = ~0u << max(pp, 0);     // positions at or after p
+  // Position p; for pp < 0 the bit lands at 32 + pp >= 32 - 3 S >= S.
+  const uint32_t at_p = 1u << (static_cast<uint32_t>(pp) & 31u);
   uint32_t na[S];
 #pragma unroll
   for (int i = 0; i < S; ++i) {
-    uint32_t v = bsel(bit_mask(to_left, i), dn1[i], up1[i]);
-    v = bsel(bit_mask(at_p, i), sum, v);
-    na[i] = bsel(bit_mask(keep, i), a[i], v);
+    uint32_t v = bsel(bit_mask1(right, i), up1[i], dn1[i]);
+    v = bsel(bit_mask1(at_p, i), sum, v);
+    na[i] = bsel(bit_mask1(from_p, i), v, a[i]);
   }
 #pragma unroll
   for (int i = 0; i < S; ++i) a[i] = na[i];
@@ -460,7 +473,8 @@ __device__ __forceinline__ void step_lm(uint32_t (&a)[CAP], int g, bool active, 
     dn1[i] = i > 0 ? a[i > 0 ? i - 1 : 0] : pv;
     up2[i] = i + 2 < S ? a[i + 2 < S ? i + 2 : 0] : (i + 2 == S ? nx0 : nx1);
   }
-  int kslot = -1;
+  const int base = g * S;
+  int kslot = 0x3FF - base;  // no qualifying slot: position 0x3FF
   uint32_t xs = 0, ys = 0;
 #pragma unroll
   for (int i = S - 1; i >= 0; --i) {
@@ -469,8 +483,7 @@ __device__ __forceinline__ void step_lm(uint32_t (&a)[CAP], int g, bool active, 
     xs = c ? a[i] : xs;
     ys = c ? up1[i] : ys;
   }
-  const int base = g * S;
-  const uint32_t kq = kslot >= 0 ? static_cast<uint32_t>(base + kslot) : 0x3FFu;
+  const uint32_t kq = static_cast<uint32_t>(base + kslot);
   const int k = static_cast<int>(quad_min(kq));
   const bool own = kq == static_cast<uint32_t>(k);
   const uint32_t x = quad_or<Item16>(own ? xs : 0u);
