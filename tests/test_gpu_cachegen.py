@@ -418,7 +418,7 @@ def _fib_counts(rng, nb, extra):
 
 
 @pytest.mark.parametrize("case", ["one_lane", "quad32", "quad64", "quad64_not_exact", "fallback_one_lane",
-                                  "fallback_quad", "long_few_counted", "long_wide_items"])
+                                  "fallback_quad", "long_few_counted", "long_wide_items", "quad_ties"])
 def test_calculate_cdf_modes_vs_oracle(ops, case):
     """calculate_cdf picks, per block of 64 streams, one lane per stream
     (at most 16 present symbols) or a quad of lanes per stream with 32- or
@@ -426,7 +426,10 @@ def test_calculate_cdf_modes_vs_oracle(ops, case):
     (Garsia-Wachs trees deeper than 8 levels), chunks longer than 256
     tokens with at most 256 counted symbols (8-bit limit) and chunks of
     65536 tokens or more (no 16-bit items) are bit-exact against the
-    oracle."""
+    oracle.  `quad_ties` gives the node-id quads equal and two- or
+    three-valued weights (several optimal trees, where the tie rule picks
+    one) and 2..32 present symbols per stream within one block, so the
+    lists of one wave end at different steps."""
     rng = np.random.default_rng(sum(map(ord, case)))
     T, nb, C = 256, 32, 128
     if case == "one_lane":
@@ -445,6 +448,23 @@ def test_calculate_cdf_modes_vs_oracle(ops, case):
     elif case == "long_few_counted":
         T = 700
         rows = [_gaussian_counts(rng, 200, 16 if c < 64 else 32, nb) for c in range(C)]
+    elif case == "quad_ties":
+        rows = []
+        for c in range(C):
+            m = 32 if c % 64 == 0 else int(rng.integers(2, 33))
+            kind = c % 4
+            if kind == 0:
+                w = [8] * m
+            elif kind == 1:
+                w = [1 + (j % 2) for j in range(m)]
+            elif kind == 2:
+                w = [int(x) for x in rng.choice([1, 2, 4], size=m)]
+            else:
+                w = [int(x) for x in rng.integers(1, 4, size=m)]
+            counts = [0] * nb
+            for pos, x in zip(sorted(rng.choice(nb, size=m, replace=False)), w):
+                counts[int(pos)] = x
+            rows.append(counts)
     else:
         T, C = 65536, 64
         rows = [[4096] * 16 + [0] * 16 for _ in range(C)]
