@@ -49,6 +49,50 @@ def test_chunk_codec_round_trip_vs_oracle(F, L, T, C, nb):
     assert np.array_equal(out.cpu().numpy(), sym)
 
 
+def _quantize_planes(x, bins):
+    """Symmetric per-(plane, channel) quantiser over a chunk's tokens into
+    [0, bins - 2] (this library's own; the reference's sits in upstream
+    LMCache)."""
+    half = (bins // 2 - 1).to(torch.float32).view(-1, 1, 1)
+    amax = x.abs().amax(dim=1, keepdim=True).clamp_min(1e-30)
+    return (torch.round(x / amax * half) + half).to(torch.uint8)
+
+
+@pytest.mark.parametrize("n_tokens", [1, 20, 256, 8000])
+@pytest.mark.parametrize("n_layers", [1, 28])
+@pytest.mark.parametrize("chunk_size", [128, 256])
+@pytest.mark.parametrize("num_heads", [1, 8])
+def test_chunked_encode_into_decode(F, n_tokens, n_layers, chunk_size, num_heads):
+    """The reference's end-to-end CacheGen test, in its parameter grid
+    (tests/v1/test_cachegen_kernels.py:242-345): bf16 K and V of
+    [n_layers, n_tokens, num_heads x 128] from N(0, 2), K layers 0-9 at 32
+    bins and the rest at 16, V layers 0-1 at 32 and the rest at 16 (one
+    layer: 32 for both), cut into chunks of chunk_size tokens; each chunk is
+    quantised, encoded, serialized, read back and decoded, and the decoded
+    symbols equal the quantised ones."""
+    torch.manual_seed(n_tokens * 7 + n_layers * 3 + chunk_size + num_heads)
+    C = num_heads * 128
+    kv = (torch.randn((n_layers, 2, n_tokens, C), device=DEV) * 2).to(torch.bfloat16)
+    if n_layers == 1:
+        kb = vb = torch.tensor([32], device=DEV)
+    else:
+        kb = torch.full((n_layers,), 16, device=DEV)
+        kb[:10] = 32
+        vb = torch.full((n_layers,), 16, device=DEV)
+        vb[:2] = 32
+    bins = torch.cat([kb, vb])
+    for t0 in range(0, n_tokens, chunk_size):
+        part = kv[:, :, t0:t0 + chunk_size].float()
+        planes = torch.cat([part[:, 0], part[:, 1]]).contiguous()  # [2L, T, C]: K layers, then V
+        sym = _quantize_planes(planes, bins)
+        chunk = F.encode_chunk(sym, 32)
+        back = F.CacheGenChunk.from_bytes(chunk.to_bytes(), device=DEV)
+        assert back.shape == (2 * n_layers, sym.shape[1], C)
+        out = F.decode_chunk(back)
+        torch.cuda.synchronize()
+        assert torch.equal(out, sym), (t0, n_tokens)
+
+
 def test_chunk_encode_refuses_cpu_symbols(F):
     with pytest.raises(ValueError):
         F.encode_chunk(torch.zeros(1, 4, 32, dtype=torch.uint8), 16)
