@@ -1071,6 +1071,7 @@ constexpr int kDecLds = 40 * 1024;
 constexpr int kL1Bytes = (1 << kDirectBits) * kDecLanes * 2;
 constexpr int kL2Bytes = kSubTables * (1 << kSubBits) * kDecLanes;
 constexpr int kObufBytes = 4 * kDecLanes;
+static_assert(kObufBytes >= 256, "the byte table build writes past the table into the 256 bytes after it");
 constexpr int kRowChunks = 5;   // 16-byte row chunks per lane and load batch (33 x 64 x 2 B)
 constexpr int kWinChunks = 12;  // 16-byte window chunks per lane and load batch (12 KiB)
 
@@ -1515,10 +1516,11 @@ __device__ __forceinline__ void decode_one_wave(uint8_t *lds, const int16_t *__r
 
 // Byte tables with per-lane stream regions (cgdec::LaneRegion): each lane
 // stages the 16-byte aligned chunks holding its own stream into its own LDS
-// region and zeroes what lies past the stream's end, so the cursor
-// (cgdec::LaneCursor, a 64-bit window refilled once per four codes of at
-// most 8 bits, each refill one byte permutation of two raw dwords) reads
-// the region without masking the stream's end.
+// region and zeroes what lies past the stream's end, so the cursors read
+// the region without masking the stream's end: cgdec::GroupCursor for
+// tables without escapes (four codes per group, windows re-read from the
+// region on a fixed schedule), cgdec::LaneCursor for the others.  The 256
+// bytes after the table (obuf) are scratch while the table is built.
 // Serves full 64-stream blocks with dword-aligned output rows whose regions
 // fit the LDS left after the tables and rows; returns false, having written
 // nothing, for any other block, which then takes decode_one_wave.
@@ -1554,7 +1556,7 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
   // Chunks [a0, a0 + 16 n_ch) each hold a byte of the stream, so no load
   // leaves the buffer's pages.
   const uint32_t n_ch = len ? static_cast<uint32_t>(((s_hi - 1) >> 4) - (s_lo >> 4) + 1) : 0u;
-  const uint32_t rbytes = 16u * n_ch + 16u;  // chunks plus 4 dwords: the zero dword and reads ahead
+  const uint32_t rbytes = 16u * n_ch + cgdec::LaneRegion::kRoom;  // chunks plus the sealed room
   uint32_t incl = rbytes, n_max = n_ch;
 #pragma unroll
   for (int d = 1; d < kDecLanes; d <<= 1) {
@@ -1599,38 +1601,41 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
   }
   uint32_t *reg32 = reinterpret_cast<uint32_t *>(region);
   cgdec::LaneRegion::seal(reg32, static_cast<uint32_t>(s_lo - a0), len);
-  cgdec::LaneCursor cur;
-  cur.start(reg32, static_cast<uint32_t>(s_lo - a0), len);
   uint8_t *obuf = lds + Tab::kBytes;
   uint8_t *out_blk = out + static_cast<int64_t>(bk.l) * T * C + bk.c0;
   // Lane j stores token (t0 + j / 16), channels 4 * (j % 16) .. + 3.
   uint32_t *odst = reinterpret_cast<uint32_t *>(out_blk + static_cast<int64_t>(lane >> 4) * C) + (lane & 15);
   const int64_t step4 = static_cast<int64_t>(C);  // in dwords: 4 tokens of C bytes
   if (!__any(tb.escapes)) {
-    // Four tokens per step: four lookups and one refill (a step starts with
-    // at least 33 valid bits and takes at most 32), the four table entries
-    // through the LDS transpose, and the transposed word of the previous
-    // step stored with its symbols extracted (entry >> 3 in every byte), so
-    // no step waits for its own transpose read.  The scheduling barrier
-    // keeps the store after the lookups: the compiler would otherwise hoist
-    // it, and its wait for the transpose read, above the first lookup.
-    // Measured on MI355X (symbol loop, shader cycles per symbol): a refill
-    // every two symbols and symbols extracted per step 158.6; the store one
-    // step late 150.4; one refill per four symbols 132.8; entries
-    // transposed 128.4.
+    // Four tokens per group (cgdec::GroupCursor): the four table entries go
+    // through the LDS transpose and the symbols of the resulting word are
+    // extracted at once, (word >> 3) & 0x1F1F1F1F; each word is stored one
+    // group late, so no group waits for its own transpose read.  The
+    // transpose writes, that store and the transposing read sit between the
+    // group's codes, each under a table read (the cursor's scheduling
+    // barriers keep them there).  Measured on MI355X (symbol loop, shader
+    // cycles per symbol, s_memtime stamps): 128-133 with the refilled lane
+    // cursor (its chain four VALU instructions and the table read, the
+    // refill on it every fourth code) -> 112 with this cursor -> 102 with
+    // the transpose spread between the codes -> 100 with the window's
+    // permutations one code later.  The chain alone, timed in isolation,
+    // takes 72 cycles; the rest is issue of the other instructions under
+    // it and LDS traffic.
+    cgdec::GroupCursor gc;
+    gc.start(tb, reg32, lds_at + static_cast<uint32_t>(region - lds), static_cast<uint32_t>(s_lo - a0), len);
     int t = 0;
     uint32_t word = 0;
     for (; t + 4 <= T; t += 4) {
-      const uint32_t e0 = tb.step8e(cur), e1 = tb.step8e(cur);
-      const uint32_t e2 = tb.step8e(cur), e3 = tb.step8e(cur);
-      cur.refill();
-      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t e0 = gc.step0(tb);
+      const uint32_t e1 = gc.step1(tb);
+      obuf[lane] = static_cast<uint8_t>(e0);
       if (t > 0) {
         cg_st(odst, (word >> 3) & 0x1F1F1F1Fu);
         odst += step4;
       }
-      obuf[lane] = static_cast<uint8_t>(e0);
+      const uint32_t e2 = gc.step2(tb);
       obuf[kDecLanes + lane] = static_cast<uint8_t>(e1);
+      const uint32_t e3 = gc.step3(tb);
       obuf[2 * kDecLanes + lane] = static_cast<uint8_t>(e2);
       obuf[3 * kDecLanes + lane] = static_cast<uint8_t>(e3);
       wave_sync();
@@ -1642,15 +1647,14 @@ __device__ __forceinline__ bool decode_one_wave_lanes(uint8_t *lds, const int16_
       odst += step4;
     }
     if (t < T) {
-      for (int i = 0; t + i < T; ++i) {
-        obuf[i * kDecLanes + lane] = static_cast<uint8_t>(tb.step8(cur));
-        if (i & 1) cur.refill();
-      }
+      for (int i = 0; t + i < T; ++i) obuf[i * kDecLanes + lane] = static_cast<uint8_t>(gc.single(tb));
       wave_sync();
       if ((lane >> 4) < T - t) cg_st(odst, reinterpret_cast<const uint32_t *>(obuf)[lane]);
     }
   } else {
     tb.finish();
+    cgdec::LaneCursor cur;
+    cur.start(reg32, static_cast<uint32_t>(s_lo - a0), len);
     auto step = [&]() -> uint8_t {
       int s, l;
       tb.lookup(cur.top16(), s, l);

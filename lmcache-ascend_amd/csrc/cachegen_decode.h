@@ -24,10 +24,17 @@ __device__ __forceinline__ uint32_t lds_dword(uint32_t at) {
 __device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
+// The low 32 bits of the 64-bit hi:lo shifted right by s % 32.
+__device__ __forceinline__ uint32_t align_bits(uint32_t hi, uint32_t lo, uint32_t s) {
+  return __builtin_amdgcn_alignbit(hi, lo, s);
+}
 // True in every lane when b holds in some lane of the wave.
 __device__ __forceinline__ bool wave_any(bool b) { return __any(b); }
 #else
 inline bool wave_any(bool b) { return b; }
+inline uint32_t align_bits(uint32_t hi, uint32_t lo, uint32_t s) {
+  return static_cast<uint32_t>(((static_cast<uint64_t>(hi) << 32) | lo) >> (s & 31u));
+}
 inline uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
   uint32_t r = 0;
@@ -135,31 +142,63 @@ struct BitCursor {
 // Per-lane stream regions.  A lane's stream, bytes [start, end) of the
 // concatenated stream buffer, is staged as the raw little-endian dwords of
 // the 16-byte aligned chunks that hold it (the first chunk starts at
-// start & ~15, so the stream begins `off` = start & 15 bytes in), with 16
-// bytes of room after them.  LaneRegion::seal zeroes what a cursor reads
-// past the stream's end (the rest of the dword holding the end and the two
-// dwords after it), so bits past the end read as zero; the cursor forms
-// the stream's big-endian dword q from raw dwords off / 4 + q and the one
-// after it with one byte permutation (swap and alignment together).
-// An empty stream takes offset 0 (its region is the 16 bytes of room, which
-// hold the dwords read at offsets 0..3 only).
+// start & ~15, so the stream begins `off` = start & 15 bytes in), with
+// kRoom bytes of room after them.  LaneRegion::seal zeroes what a cursor
+// reads past the stream's end (the rest of the dword holding the end and
+// the four dwords after it), so bits past the end read as zero; a cursor
+// forms the stream's big-endian dword q from raw dwords off / 4 + q and the
+// one after it with one byte permutation (swap and alignment together).
+// Stream dwords from n_dw = ceil(len / 4) on read as zero through raw
+// dwords n_dw .. n_dw + 3 (past off / 4), all inside the sealed part.
+// An empty stream takes offset 0 (its region is the room alone).
 struct LaneRegion {
+  static constexpr uint32_t kRoom = 32;
   static __device__ __forceinline__ void seal(uint32_t *region, uint32_t off, uint32_t len) {
     off = len ? off : 0u;
     const uint32_t e = off + len, i = e >> 2, keep = e & 3u;
     region[i] &= keep ? 0xFFFFFFFFu >> (32u - 8u * keep) : 0u;
     region[i + 1] = 0u;
     region[i + 2] = 0u;
+    region[i + 3] = 0u;
+    region[i + 4] = 0u;
   }
 };
 
-// Bit cursor over a sealed lane region: a 64-bit window whose top `have`
-// bits are the stream's next bits (zeros past the end are real zeros), and
-// `next`, the stream dword to append, read ahead.  refill() appends it when
-// 32 bits or fewer are left, so after a refill more than 32 bits are valid:
-// four codes of at most 8 bits, or two of at most 16, can be taken between
-// refills.  Stream dword k reads raw dwords min(k, n_dw) + off / 4 and the
-// one after; from n_dw = ceil(len / 4) on that is sealed zeros.
+// 64-bit windows of a sealed lane region: at(q) is the 64 stream bits from
+// stream bit q (big-endian: the top bit is bit q), zeros past the stream's
+// end.  Stream dwords j, j + 1, j + 2 (j = q / 32, clamped to n_dw, where
+// every dword reads as zero) come from raw dwords j .. j + 3 by three byte
+// permutations, and the window is their top 64 bits after a shift by
+// q % 32, two 64-bit shifts.
+struct LaneWindows {
+  const uint32_t *w;  // raw region + off / 4
+  uint32_t sel;       // byte permutation for the stream's offset in its dword
+  uint32_t zl;        // n_dw
+
+  __device__ __forceinline__ void start(const uint32_t *region, uint32_t off, uint32_t len) {
+    off = len ? off : 0u;
+    w = region + (off >> 2);
+    sel = 0x00010203u + (off & 3u) * 0x01010101u;
+    zl = (len + 3u) >> 2;
+  }
+  __device__ __forceinline__ uint64_t at(uint32_t q) const {
+    const uint32_t j = (q >> 5) < zl ? (q >> 5) : zl;
+    const uint32_t r0 = w[j], r1 = w[j + 1u], r2 = w[j + 2u], r3 = w[j + 3u];
+    const uint32_t a = byte_perm(r1, r0, sel), b = byte_perm(r2, r1, sel), c = byte_perm(r3, r2, sel);
+    const uint32_t o = q & 31u;
+    const uint64_t ab = (static_cast<uint64_t>(a) << 32) | b, bc = (static_cast<uint64_t>(b) << 32) | c;
+    return ((ab << o) & 0xFFFFFFFF00000000ull) | ((bc << o) >> 32);
+  }
+};
+
+// Bit cursor over a sealed lane region for tables with escapes (codes of
+// up to 16 bits): a 64-bit window whose top `have` bits are the stream's
+// next bits (zeros past the end are real zeros), and `next`, the stream
+// dword to append, read ahead.  refill() appends it when 32 bits or fewer
+// are left, so after a refill more than 32 bits are valid: two codes of at
+// most 16 bits can be taken between refills.  Stream dword k reads raw
+// dwords min(k, n_dw) + off / 4 and the one after; from n_dw = ceil(len / 4)
+// on that is sealed zeros.
 struct LaneCursor {
   const uint32_t *w;  // raw region + off / 4
   uint32_t sel;       // byte permutation for the stream's offset in its dword
@@ -187,7 +226,6 @@ struct LaneCursor {
     q = 2u;
     fetch(q);
   }
-  __device__ __forceinline__ uint32_t top8() const { return static_cast<uint32_t>(win >> 56); }
   __device__ __forceinline__ uint32_t top16() const { return static_cast<uint32_t>(win >> 48); }
   __device__ __forceinline__ void consume(int n) {
     win <<= n;
@@ -259,29 +297,32 @@ struct ByteTables {
     for (int d = 0; d < 64; ++d) t32[d * kLanes] = 0;
   }
 
-  // Writes the entries of the cleared table and sets row.wrap.  The row is
-  // read into registers (kMaxBins entries whatever nb is: entries past the
-  // row are garbage and lie past the wrap); a first pass finds the wrap,
-  // the first symbol whose base is below an earlier one, or nb; every
-  // symbol from the wrap on has base 0x10000 and writes nothing.  Writes
-  // that fall outside the table go to `dummy`, a byte of the caller's, so
-  // the loops have no branches.  When no row of the wave has a base off a
-  // multiple of 256 (calculate_cdf's rows; checked for nb == kMaxBins, where
-  // every loaded entry belongs to the row), no base writes an escape, and
-  // the loop without those writes is taken.
+  // Writes the entries of the cleared table.  The row is read into
+  // registers (kMaxBins entries whatever nb is: entries past the row are
+  // garbage and lie past the wrap).  Bases are taken in symbol order with a
+  // sticky flag: from the wrap on (the first symbol whose base is below the
+  // one before it, or nb), every base is 0x10000, which writes nothing.
+  // Writes that fall outside the table go to `dummy`, a byte of the
+  // caller's, so the loops have no branches.  When no row of the wave has a
+  // base off a multiple of 256 (calculate_cdf's rows; checked for nb ==
+  // kMaxBins, where every loaded entry belongs to the row), no base writes
+  // an escape, and the loop without those writes is taken; its writes past
+  // the table (base 0x10000: entry 256) land in the 256 bytes after the
+  // table, which the caller keeps as scratch while the table is built.
   __device__ __forceinline__ void mark(uint8_t *dummy) {
-    uint32_t rw[kMaxBins];
+    uint32_t rw[kMaxBins], eff[kMaxBins];
 #pragma unroll
     for (int s = 0; s < kMaxBins; ++s) rw[s] = static_cast<uint16_t>(row.r[s]);
-    int wrap = nb;
-    uint32_t top_base = rw[0] & 0xFFF0u;
+    bool wrapped = false;
+    uint32_t prev = rw[0] & 0xFFF0u;
+    eff[0] = prev;
 #pragma unroll
     for (int s = 1; s < kMaxBins; ++s) {
       const uint32_t v = rw[s] & 0xFFF0u;
-      wrap = min(wrap, v < top_base ? s : kMaxBins);
-      top_base = max(top_base, v);
+      wrapped = wrapped || v < prev || s >= nb;
+      eff[s] = wrapped ? 0x10000u : v;
+      prev = v;
     }
-    row.wrap = wrap;
     bool aligned = false;
     if (nb == kMaxBins) {
       uint32_t acc = 0;
@@ -290,35 +331,35 @@ struct ByteTables {
       aligned = !wave_any((acc & 0xF0u) != 0);
     }
     if (aligned)
-      mark_rows<true>(rw, wrap, dummy);
+      mark_rows<true>(rw, eff, dummy);
     else
-      mark_rows<false>(rw, wrap, dummy);
+      mark_rows<false>(rw, eff, dummy);
   }
 
   template <bool kAligned>
-  __device__ __forceinline__ void mark_rows(const uint32_t (&rw)[kMaxBins], int wrap, uint8_t *dummy) {
-    uint32_t base = rw[0] & 0xFFF0u;
+  __device__ __forceinline__ void mark_rows(const uint32_t (&rw)[kMaxBins], const uint32_t (&eff)[kMaxBins],
+                                            uint8_t *dummy) {
 #pragma unroll
     for (int s = 0; s < kMaxBins; ++s) {
-      const uint32_t next = s + 1 < wrap ? rw[s + 1 < kMaxBins ? s + 1 : 0] & 0xFFF0u : 0x10000u;
+      const uint32_t base = eff[s];
+      const uint32_t next = s + 1 < kMaxBins ? eff[s + 1 < kMaxBins ? s + 1 : 0] : 0x10000u;
       const uint32_t nib = rw[s] & 0xFu;
-      const uint32_t w = next - base;
-      // 16 - floor(log2 w); w = 0 gives 17, an escape.
-      const uint32_t wl = static_cast<uint32_t>(w != 0 ? __builtin_clz(w) : 32) - 15u;
+      // 16 - floor(log2 w); w = 0 gives 16, an escape.
+      const uint32_t wl = static_cast<uint32_t>(__builtin_clz((next - base) | 1u)) - 15u;
       const uint32_t len = nib != 0 ? nib : wl;
       const uint32_t code = len - 1u < 8u ? ((static_cast<uint32_t>(s) << 3) | (len - 1u)) : kEscape;
       if (s == 0) {  // owns the windows below every later base: prefix 0
         *entry(0) = static_cast<uint8_t>(code);
       } else if (kAligned) {
-        // base is a multiple of 256, or 0x10000 from the wrap on (no entry).
-        *(base < 0x10000u ? entry(base >> 8) : dummy) = static_cast<uint8_t>(code);
+        // base is a multiple of 256 (entry base / 256), or 0x10000 from
+        // the wrap on (entry 256, past the table).
+        *(tab + ((base >> 2) & 0x7F00u) + ((base >> 8) & 3u)) = static_cast<uint8_t>(code);
       } else {
         // base is 0x10000 from the wrap on: no escape (its low byte is 0)
         // and no entry (it is not below 0xFF01).
         *((base & 0xFFu) ? entry(base >> 8) : dummy) = static_cast<uint8_t>(kEscape);
         *(base < 0xFF01u ? entry((base + 0xFFu) >> 8) : dummy) = static_cast<uint8_t>(code);
       }
-      base = next;
     }
   }
 
@@ -363,10 +404,18 @@ struct ByteTables {
     escapes = (prev >> 24) == kEscape;
   }
 
-  // top, which only the binary search reads.
+  // top and row.wrap, which only the binary search reads.
   __device__ __forceinline__ void finish() {
     top = 1;
     while (top * 2 < nb) top *= 2;
+    int wrap = nb;
+    uint32_t top_base = static_cast<uint16_t>(row.r[0]) & 0xFFF0u;
+    for (int s = 1; s < kMaxBins; ++s) {
+      const uint32_t v = static_cast<uint16_t>(row.r[s]) & 0xFFF0u;
+      wrap = min(wrap, v < top_base ? s : kMaxBins);
+      top_base = max(top_base, v);
+    }
+    row.wrap = wrap;
   }
 
   // Builds the table after clear().
@@ -384,42 +433,6 @@ struct ByteTables {
     return x;
   }
 
-  // One symbol at a lane cursor for a table without escapes; returns the
-  // symbol.  At most 8 bits are taken.  The entry is taken from the dword
-  // holding entries 4 (e / 4) .. + 3, whose address needs only the window's
-  // top 6 bits, so the chain from one symbol to the next is two operations
-  // before the LDS read and a bit-field extract and a shift after it.
-  __device__ __forceinline__ uint32_t step8(LaneCursor &cur) const {
-    const uint32_t hi = static_cast<uint32_t>(cur.win >> 32);
-    // dword (e / 4) of the lane's column: table byte offset (e / 4) * 256 +
-    // lane * 4, with e / 4 the window's top 6 bits; the table's LDS address
-    // is a multiple of its 16 KiB size, so the offset is ORed in.
-    const uint32_t at = ((hi >> 18) & 0x3F00u) | lane_at;
-    const uint32_t d = lds_dword(at);
-    const uint32_t sh = (hi >> 21) & 0x18u;  // 8 * (e % 4)
-    // Every code takes at least one bit: that shift does not wait for the
-    // entry, the rest (length - 1) does.
-    cur.win <<= 1;
-    cur.win <<= (d >> sh) & 7u;
-    cur.have -= static_cast<int>((d >> sh) & 7u) + 1;
-    return (d >> (sh | 3u)) & 31u;
-  }
-
-  // step8 for the transposing loop: returns the table entry in the low
-  // byte (symbol << 3 | length - 1; the higher bytes hold other entries),
-  // whose symbols the caller extracts four at a time, one word per four
-  // tokens, instead of one symbol per step.
-  __device__ __forceinline__ uint32_t step8e(LaneCursor &cur) const {
-    const uint32_t hi = static_cast<uint32_t>(cur.win >> 32);
-    const uint32_t d = lds_dword(((hi >> 18) & 0x3F00u) | lane_at);
-    const uint32_t sh = (hi >> 21) & 0x18u;
-    const uint32_t l = (d >> sh) & 7u;
-    cur.win <<= 1;
-    cur.win <<= l;
-    cur.have -= static_cast<int>(l) + 1;
-    return d >> sh;
-  }
-
   // Symbol and code length for the 16-bit window v.
   __device__ __forceinline__ void lookup(uint32_t v, int &s, int &len) const {
     const uint32_t b = tab[((v >> 10) << 8) + ((v >> 8) & 3u)];
@@ -432,6 +445,141 @@ struct ByteTables {
         if (s + step < nb && row.base(s + step) <= v) s += step;
       len = row.len(s);
     }
+  }
+};
+
+// Cursor for byte tables without escapes over a sealed lane region
+// (LaneWindows), four codes per group.  The chain from one code to the next
+// is the table read and three VALU instructions: the entry's length field
+// and the next code's table dword, addressed from the current code's window
+// bits (the next window is this one shifted by length bits, so its top six
+// bits are bits 62 - l .. 57 - l of this one, l = length - 1, which
+// y = h >> 17 holds at 13 - l .. 8 - l: ((y << l) & 0x3F00) | lane_at).
+// The rest, each code's window bits h (from which y and the byte's shift sh
+// in its table dword) and the windows, is kept off that chain: h is taken
+// from a 64-bit window v at offset o, and a group reads the window at its
+// second code's stream bit, vn, and switches to it at its fourth code, so
+// no window is refilled by a data-dependent shift.  v serves the codes from
+// the fourth of the previous group to the third of this one (offsets up to
+// 40); the next code's address needs 6 + l bits past the current code, so
+// every bit read lies within the window's 64.  Scheduling barriers keep
+// each chain (the wait for the entry, three instructions, the next read)
+// free of other instructions, which are placed while a read is in flight.
+struct GroupCursor {
+  LaneWindows lw;
+  uint32_t wa;  // LDS address of lw.w (raw region + off / 4)
+  uint64_t v;   // window at stream bit qm + 1
+  uint32_t qm;
+  uint32_t o;   // offset in v of the current code
+  uint32_t y;   // the current code's window bits 31 .. 17 (h >> 17)
+  uint32_t sh;  // 8 x the current code's byte in its table dword
+  uint32_t d;   // the current code's table dword (its read in flight)
+  // The next window (read during a group): its stream bit less one, the
+  // offset in v it starts at, its raw dwords, then its stream dwords, then
+  // the window.
+  uint32_t qn1, o1, r0, r1, r2, r3, a, b, c;
+  uint64_t vn;
+
+  static __device__ __forceinline__ void fence() {
+#ifdef __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  }
+
+  __device__ __forceinline__ void place(uint64_t nv) {
+    const uint32_t h = static_cast<uint32_t>((nv << o) >> 32);
+    y = h >> 17;
+    sh = (h >> 21) & 0x18u;
+  }
+
+  // region_at: the LDS address of region.
+  __device__ __forceinline__ void start(const ByteTables &tb, const uint32_t *region, uint32_t region_at,
+                                        uint32_t off, uint32_t len) {
+    lw.start(region, off, len);
+    wa = region_at + 4u * static_cast<uint32_t>(lw.w - region);
+    qm = 0xFFFFFFFFu;
+    v = lw.at(0);
+    o = 0;
+    place(v);
+    d = lds_dword(((static_cast<uint32_t>(v >> 32) >> 18) & 0x3F00u) | tb.lane_at);
+  }
+
+  // The chain: the current code's length from its entry and the next code's
+  // table read.  Returns the length - 1; e is the entry in the low byte.
+  __device__ __forceinline__ uint32_t advance(const ByteTables &tb, uint32_t &e) {
+    fence();
+    const uint32_t dc = d;
+    const uint32_t l = (dc >> sh) & 7u;
+    d = lds_dword(((y << l) & 0x3F00u) | tb.lane_at);
+    fence();
+    e = dc >> sh;
+    return l;
+  }
+
+  // The four codes of a group, each returning its entry; a caller may place
+  // its own work between them (it lands under a table read).
+  __device__ __forceinline__ uint32_t step0(const ByteTables &tb) {
+    uint32_t e;
+    const uint32_t l = advance(tb, e);
+    o += l + 1u;
+    place(v);
+    // The next window's raw dwords, from stream bit qn1 + 1 (LaneWindows::at
+    // with the bit less one: dwords j = qn1 / 32 on, shifted by
+    // 31 - qn1 % 32, one alignbit per word): loads issued here.
+    o1 = o;
+    qn1 = qm + o1;
+    const uint32_t j = (qn1 >> 5) < lw.zl ? (qn1 >> 5) : lw.zl;
+    const uint32_t at = wa + (j << 2);
+    r0 = lds_dword(at);
+    r1 = lds_dword(at + 4u);
+    r2 = lds_dword(at + 8u);
+    r3 = lds_dword(at + 12u);
+    return e;
+  }
+  __device__ __forceinline__ uint32_t step1(const ByteTables &tb) {
+    uint32_t e;
+    const uint32_t l = advance(tb, e);
+    o += l + 1u;
+    place(v);
+    return e;
+  }
+  __device__ __forceinline__ uint32_t step2(const ByteTables &tb) {
+    uint32_t e;
+    const uint32_t l = advance(tb, e);
+    a = byte_perm(r1, r0, lw.sel);
+    b = byte_perm(r2, r1, lw.sel);
+    c = byte_perm(r3, r2, lw.sel);
+    const uint32_t sr = ~qn1;
+    vn = (static_cast<uint64_t>(align_bits(a, b, sr)) << 32) | align_bits(b, c, sr);
+    o += l + 1u - o1;
+    place(vn);
+    return e;
+  }
+  __device__ __forceinline__ uint32_t step3(const ByteTables &tb) {
+    uint32_t e;
+    const uint32_t l = advance(tb, e);
+    o += l + 1u;
+    place(vn);
+    v = vn;
+    qm = qn1;
+    return e;
+  }
+  __device__ __forceinline__ void group(const ByteTables &tb, uint32_t &e0, uint32_t &e1, uint32_t &e2,
+                                        uint32_t &e3) {
+    e0 = step0(tb);
+    e1 = step1(tb);
+    e2 = step2(tb);
+    e3 = step3(tb);
+  }
+
+  // One code read from a fresh window (the tail after the groups); returns
+  // its symbol.
+  __device__ __forceinline__ uint32_t single(const ByteTables &tb) {
+    const uint32_t hh = static_cast<uint32_t>(lw.at(qm + 1u + o) >> 32);
+    const uint32_t s8 = (hh >> 21) & 0x18u;
+    const uint32_t e = lds_dword(((hh >> 18) & 0x3F00u) | tb.lane_at) >> s8;
+    o += (e & 7u) + 1u;
+    return (e >> 3) & 31u;
   }
 };
 

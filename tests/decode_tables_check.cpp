@@ -5,11 +5,15 @@
 //
 // For every row: the table is built as the decode kernel builds it (clear,
 // mark, scan, plus finish for the binary search), and several streams are
-// decoded with the cursor: through ByteTables::step when the table holds no
-// escape entry (the kernel's branch-free loop) and through
-// ByteTables::lookup otherwise.  Each stream sits in a window of big-endian
-// dwords between other streams' bytes, at a random byte offset, so reads past
-// its end meet foreign bytes that must read as zero.
+// decoded with each cursor.  The shared-window cursor: through
+// ByteTables::step when the table holds no escape entry (the kernel's
+// branch-free loop) and through ByteTables::lookup otherwise; each stream
+// sits in a window of big-endian dwords between other streams' bytes, at a
+// random byte offset, so reads past its end meet foreign bytes that must
+// read as zero.  The lane-region cursors: the lane cursor on every table,
+// and the group cursor (GroupCursor) on tables without escapes, over the
+// stream's own sealed region, sized exactly as in the kernel (built with
+// AddressSanitizer, a read past it fails the run).
 //
 // Usage: decode_tables_check <rows> <seed>; prints "ok ..." or the first
 // mismatch and exits 1.
@@ -78,7 +82,7 @@ void make_row(std::mt19937_64 &rng, int nb, int kind, int16_t *row) {
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? atoi(argv[1]) : 2000;
   std::mt19937_64 rng(argc > 2 ? strtoull(argv[2], nullptr, 10) : 1);
-  static uint8_t lds[ByteTables::kBytes];
+  static uint8_t lds[ByteTables::kBytes + 256];  // the table and the 256 scratch bytes after it
   uint8_t dummy = 0;
   long long symbols = 0, fast_rows = 0, escaped_rows = 0;
   for (int it = 0; it < rows; ++it) {
@@ -135,37 +139,29 @@ int main(int argc, char **argv) {
         }
       // The lane-region path: the stream's 16-byte aligned chunks of the
       // byte buffer (foreign bytes around it) as raw little-endian dwords,
-      // plus 4 garbage dwords, sealed past the stream's end, then decoded
-      // with the lane cursor: two codes per refill without escapes, one with.
+      // plus LaneRegion::kRoom bytes of garbage, sealed past the stream's
+      // end.  Every table is decoded with the lane cursor (one code per
+      // refill, binary search on escapes), and tables without escapes also
+      // with the group cursor, as the kernel does: four codes per group,
+      // single codes for the tail.
       {
         const uint32_t a0 = lo & ~15u;
         const uint32_t n_ch = len ? ((hi - 1) / 16 - lo / 16 + 1) : 0;
-        std::vector<uint32_t> region(4 * n_ch + 4);
+        std::vector<uint32_t> region(4 * n_ch + lmc::cgdec::LaneRegion::kRoom / 4);
         for (auto &x : region) x = static_cast<uint32_t>(rng());
         for (uint32_t i = 0; i < 16 * n_ch; ++i)
           reinterpret_cast<uint8_t *>(region.data())[i] = win_bytes[a0 + i];
         lmc::cgdec::LaneRegion::seal(region.data(), lo - a0, len);
         lmc::cgdec::LaneCursor lc;
         lc.start(region.data(), lo - a0, len);
-        int t = 0;
-        if (!tb.escapes) {
-          for (; t + 2 <= T; t += 2) {
-            got[t] = static_cast<uint8_t>(tb.step8(lc));
-            got[t + 1] = static_cast<uint8_t>(tb.step8(lc));
-            lc.refill();
-          }
-          if (t < T) {
-            got[t] = static_cast<uint8_t>(tb.step8(lc));
-            lc.refill();
-          }
-        } else {
-          for (; t < T; ++t) {
-            int s, l;
-            tb.lookup(lc.top16(), s, l);
-            got[t] = static_cast<uint8_t>(s);
-            lc.consume(l);
-            lc.refill();
-          }
+        ByteTables ts = tb;
+        ts.finish();
+        for (int t = 0; t < T; ++t) {
+          int s, l;
+          ts.lookup(lc.top16(), s, l);
+          got[t] = static_cast<uint8_t>(s);
+          lc.consume(l);
+          lc.refill();
         }
         for (int u = 0; u < T; ++u)
           if (got[u] != want[u]) {
@@ -173,21 +169,31 @@ int main(int argc, char **argv) {
                    nb, kind, tb.escapes ? 1 : 0, k, u, got[u], want[u]);
             return 1;
           }
-        // The kernel's four-token steps: four entries, one refill, symbols
-        // taken from the entries (entry >> 3); single steps for the tail.
         if (!tb.escapes) {
-          lc.start(region.data(), lo - a0, len);
-          for (t = 0; t + 4 <= T; t += 4) {
-            for (int j = 0; j < 4; ++j) got[t + j] = static_cast<uint8_t>((tb.step8e(lc) >> 3) & 31u);
-            lc.refill();
+          // The table, its 256 scratch bytes and the region in one buffer
+          // addressed from 0 (LDS addresses), the region at its end, so a
+          // read past the region fails the run.
+          const size_t rb = region.size() * 4;
+          std::vector<uint8_t> mem(ByteTables::kBytes + 256 + rb);
+          memcpy(mem.data(), lds, ByteTables::kBytes + 256);
+          memcpy(mem.data() + ByteTables::kBytes + 256, region.data(), rb);
+          lmc::cgdec::host_lds_base() = mem.data();
+          ByteTables tg = tb;
+          tg.bind(mem.data(), static_cast<int>(tb.lane_at / 4), 0);
+          lmc::cgdec::GroupCursor gc;
+          gc.start(tg, reinterpret_cast<const uint32_t *>(mem.data() + ByteTables::kBytes + 256),
+                   ByteTables::kBytes + 256, lo - a0, len);
+          int t = 0;
+          for (; t + 4 <= T; t += 4) {
+            uint32_t e[4];
+            gc.group(tg, e[0], e[1], e[2], e[3]);
+            for (int j = 0; j < 4; ++j) got[t + j] = static_cast<uint8_t>((e[j] >> 3) & 31u);
           }
-          for (int i = 0; t < T; ++t, ++i) {
-            got[t] = static_cast<uint8_t>(tb.step8(lc));
-            if (i & 1) lc.refill();
-          }
+          for (; t < T; ++t) got[t] = static_cast<uint8_t>(gc.single(tg));
+          lmc::cgdec::host_lds_base() = lds;
           for (int u = 0; u < T; ++u)
             if (got[u] != want[u]) {
-              printf("STEP4 MISMATCH row %d (nb %d, kind %d) stream %d token %d: got %d want %d\n", it, nb, kind, k,
+              printf("GROUP MISMATCH row %d (nb %d, kind %d) stream %d token %d: got %d want %d\n", it, nb, kind, k,
                      u, got[u], want[u]);
               return 1;
             }
