@@ -39,13 +39,27 @@ using lmc::cgdec::ByteTables;
 namespace {
 
 // A CDF row of one of several kinds: calculate_cdf-like (aligned power-of-
-// two intervals of lengths 1..8 with gaps and absent symbols), sorted bases
-// in steps of 16 with random length nibbles, fully random entries, and any
-// of these with a decreasing entry (a wrap).
+// two intervals of lengths 1..8 with gaps and absent symbols; kind 3 starts
+// with codes that end exactly at prefix 127, then a gap), sorted bases in
+// steps of 16 with random length nibbles, fully random entries, and any of
+// these with a decreasing entry (a wrap).
 void make_row(std::mt19937_64 &rng, int nb, int kind, int16_t *row) {
-  if (kind == 0) {
+  if (kind == 0 || kind == 3) {
     uint32_t pos = 0;
-    for (int s = 0; s < nb; ++s) {
+    int s0 = 0;
+    if (kind == 3) {
+      // Codes of lengths 2, 3, .., 8, 8 fill prefixes 0 .. 127 exactly, the
+      // last one a single prefix at 127, and a gap follows: the prefixes
+      // after it take prefix 127's entry across the middle of the table
+      // (the table's running maximum carries it over a dword boundary).
+      for (int l = 2; l <= 9 && s0 < nb; ++l, ++s0) {
+        const int len = l < 9 ? l : 8;
+        row[s0] = static_cast<int16_t>(static_cast<uint16_t>(pos | static_cast<uint32_t>(len)));
+        pos += 1u << (16 - len);
+      }
+      pos += 256u << (rng() % 6);
+    }
+    for (int s = s0; s < nb; ++s) {
       if (rng() % 5 == 0) {  // absent: the next present base, length 0
         row[s] = static_cast<int16_t>(static_cast<uint16_t>(pos & 0xFFF0u));
         continue;
@@ -61,6 +75,8 @@ void make_row(std::mt19937_64 &rng, int nb, int kind, int16_t *row) {
       row[s] = static_cast<int16_t>(static_cast<uint16_t>(pos | static_cast<uint32_t>(l)));
       pos += w;
       if (rng() % 6 == 0) pos = std::min(0x10000u, pos + (256u << (rng() % 6)));
+      // Sometimes a gap right after a code ending at 0x8000.
+      if (pos == 0x8000u && rng() % 2) pos += 256u << (rng() % 5);
     }
   } else if (kind == 1) {
     std::vector<uint32_t> b(nb);
@@ -89,7 +105,8 @@ int main(int argc, char **argv) {
     // Every third row has kMaxBins symbols: with aligned bases (kind 0) it
     // takes mark's loop without escape writes.
     const int nb = it % 3 == 1 ? ByteTables::kMaxBins : 1 + static_cast<int>(rng() % ByteTables::kMaxBins);
-    const int kind = it % 4 == 3 ? static_cast<int>(rng() % 3) : it % 3;
+    int kind = it % 4 == 3 ? static_cast<int>(rng() % 3) : it % 3;
+    if (nb == ByteTables::kMaxBins && kind == 0 && it % 2 == 0) kind = 3;
     // The kernel reads kMaxBins row entries whatever nb is; the row lives in a
     // larger buffer of foreign entries, as in the kernel's staged rows.
     std::vector<int16_t> buf(ByteTables::kMaxBins + 8);
